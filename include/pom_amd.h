@@ -1,0 +1,152 @@
+/*
+ * pom_amd — C ABI of the MI355X (gfx950) Polynomial Mixer kernels.
+ *
+ * Plain pointers and sizes only; every device pointer refers to memory on the
+ * device that is current on the calling thread, and every launch is enqueued on
+ * `stream` (a hipStream_t passed as void*; NULL = the null stream).  No entry
+ * point synchronises, allocates or frees.  Results are deterministic: all
+ * reductions are fixed-order (no floating-point atomics).
+ *
+ * Return value: POM_OK (0) or an error code; pom_last_error() describes the
+ * last failure on the calling thread.  Invalid arguments are rejected before
+ * anything is launched.
+ *
+ * Workspace: entry points that reduce across workgroups take a workspace of
+ * at least the size the matching *_workspace_size() reports.  Its first
+ * POM_COUNTER_BYTES bytes hold arrival counters which must be zero before the
+ * first use; every call that returns POM_OK leaves them zero again, so one
+ * zero-initialised workspace can be reused by any sequence of calls on one
+ * stream.  Calls that overlap in time must not share a workspace.
+ *
+ * Layouts (element strides; the last axis is always contiguous):
+ *   x, grad_x, y_s, sh ...  (B, N, C) views  -> pom_view {data, stride_b, stride_n}
+ *   coeff, grad_coeff       (P, K) fp32 row-major
+ *   aggregate outputs       (B, G, P) contiguous, G = N / frame_len
+ *   mask, count             (B, N) fp32 weights (1 = keep), (B,) fp32
+ */
+#ifndef POM_AMD_H
+#define POM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define POM_AMD_ABI_VERSION 1
+#define POM_COUNTER_BYTES (1u << 20)
+#define POM_MAX_DEGREE 16
+
+typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
+typedef enum { POM_ROPE_NONE = 0, POM_ROPE_1D = 1, POM_ROPE_2D = 2 } pom_rope_kind;
+typedef enum {
+  POM_OK = 0,
+  POM_ERR_INVALID = 1,      /* bad shape, stride, pointer or argument   */
+  POM_ERR_UNSUPPORTED = 2,  /* valid but outside what the kernels cover */
+  POM_ERR_WORKSPACE = 3,    /* workspace missing or too small           */
+  POM_ERR_DEVICE = 4        /* the HIP runtime reported an error        */
+} pom_status;
+
+/* A (B, N, C) view with unit stride on the last axis. Strides in elements. */
+typedef struct pom_view {
+  void* data;
+  int64_t stride_b;
+  int64_t stride_n;
+} pom_view;
+
+/* Rotary tables (fp32) and integer token positions.
+ *   1-D: cos0/sin0 (rows0, P/2), pos[n * pos_stride]           (pom/pom_rope.py:93-117, :152-180)
+ *   2-D: cos0/sin0 rows (rows0, P/4), cos1/sin1 columns (rows1, P/4),
+ *        pos[n * pos_stride + 0] = row, pos[n * pos_stride + 1] = column
+ *                                                               (pom/pom_rope.py:120-149, :183-235)
+ * Positions outside [0, rows) are clamped to the table. */
+typedef struct pom_rope {
+  int kind;                 /* pom_rope_kind */
+  const float* cos0;
+  const float* sin0;
+  const float* cos1;
+  const float* sin1;
+  int64_t table_stride;
+  int64_t rows0;
+  int64_t rows1;
+  const int64_t* pos;
+  int64_t pos_stride;
+} pom_rope;
+
+int pom_abi_version(void);
+const char* pom_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Aggregation: h = act(x), p = sum_{j<K} coeff[:, j] h^(j+1), aggregated over
+ * tokens.  Modes, selected by the arguments:
+ *   mean         mask == NULL, frame_len == N, rope == NULL/NONE
+ *                replaces poly_agg_mean_triton            (pom/pom_triton.py:383-403)
+ *   masked mean  mask != NULL (frame_len == N): sum m*p / sum m, an all-zero
+ *                row gives 0; tokens with m == 0 are never read
+ *                replaces poly_agg_masked_triton          (pom/pom_triton_masked.py:402-428)
+ *   frame-causal frame_len < N: output row f = running mean of the frame
+ *                means of frames 0..f, carried in the element type after
+ *                each frame — the recurrence of PoM.state_forward
+ *                (pom/pom.py:233-262) applied to N/frame_len frames at once,
+ *                equal to full_mask_mixer with a block-causal 3-D mask
+ *                (pom/pom.py:41-45) up to that rounding
+ *   state carry  carry != NULL: (B, P) previous 'h' in the element type and
+ *                n_past previous calls; frame 0 continues that recurrence
+ *   RoPE         rope->kind 1-D / 2-D: each token's p is rotated before it is
+ *                aggregated — replaces poly_agg_rope_mean_triton
+ *                (pom/pom_triton_rope.py:985-1017) and the 2-D PyTorch route
+ *                (pom/pom_rope.py:511-515)
+ * ------------------------------------------------------------------------ */
+size_t pom_agg_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int K,
+                              int64_t frame_len, int rope_kind, int backward);
+
+/* Forward.  out: (B, N/frame_len, P) in dtype.  count_out: (B,) fp32 sum of
+ * mask weights (masked mode; may be NULL). */
+int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
+                const pom_view* x, const float* coeff,
+                const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
+                int64_t frame_len, const void* carry, int64_t n_past,
+                const pom_rope* rope,
+                void* out, float* count_out,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Backward.  grad_out: (B, N/frame_len, P) fp32.  count: (B,) fp32 from the
+ * forward (masked mode).  grad_x: view written for every token (0 where the
+ * mask is 0); may alias a slice of a larger buffer (e.g. the h-half of dY).
+ * grad_coeff: (P, K) fp32, overwritten.  The gradient of `carry` is
+ * n_past * sum_f grad_out[f] / (n_past + f + 1) and is left to the caller. */
+int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
+                const pom_view* x, const float* coeff,
+                const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
+                const float* count,
+                int64_t frame_len, int64_t n_past,
+                const pom_rope* rope,
+                const float* grad_out, const pom_view* grad_x, float* grad_coeff,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Gating (pom/pom.py:207, :103-122; query-side RoPE pom/pom_rope.py:522):
+ *   sh = R(pos) hardsigmoid(y_s + bias) * hagg[b, n / (N / groups)]
+ * hagg: (B, groups, P) fp32.  bias: (P,) fp32 or NULL.
+ * ------------------------------------------------------------------------ */
+size_t pom_gate_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t groups,
+                               int rope_kind);
+
+int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P,
+                 const pom_view* ys, const float* bias, const float* hagg, int64_t groups,
+                 const pom_rope* rope, const pom_view* sh, void* stream);
+
+/* Backward.  grad_ys: view (e.g. the s-half of dY) receiving dL/dy_s.
+ * grad_hagg: (B, groups, P) fp32.  grad_bias: (P,) fp32 or NULL. */
+int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P,
+                 const pom_view* ys, const float* bias, const float* hagg, int64_t groups,
+                 const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
+                 float* grad_hagg, float* grad_bias,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POM_AMD_H */

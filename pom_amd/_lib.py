@@ -1,0 +1,190 @@
+"""ctypes binding of libpom_amd.so, the C ABI declared in include/pom_amd.h.
+
+The shared library is built in-tree (``python pom_amd/csrc/build.py``) and
+loaded lazily on first use.  There is no fallback: if the library is missing
+or fails to load, every entry point raises.  torch is imported first so that
+the library binds to the HIP runtime torch already loaded.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("POM_AMD_LIB", os.path.join(_HERE, "libpom_amd.so"))
+
+POM_OK = 0
+POM_ERR_INVALID = 1
+POM_ERR_UNSUPPORTED = 2
+POM_ERR_WORKSPACE = 3
+POM_ERR_DEVICE = 4
+
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
+COUNTER_BYTES = 1 << 20
+MAX_DEGREE = 16
+
+# Every symbol include/pom_amd.h declares, with its ctypes signature.
+_c_i64 = ctypes.c_int64
+_c_vp = ctypes.c_void_p
+_c_int = ctypes.c_int
+_c_size = ctypes.c_size_t
+
+
+class PomView(ctypes.Structure):
+    _fields_ = [("data", _c_vp), ("stride_b", _c_i64), ("stride_n", _c_i64)]
+
+
+class PomRope(ctypes.Structure):
+    _fields_ = [("kind", _c_int), ("cos0", _c_vp), ("sin0", _c_vp), ("cos1", _c_vp), ("sin1", _c_vp),
+                ("table_stride", _c_i64), ("rows0", _c_i64), ("rows1", _c_i64), ("pos", _c_vp),
+                ("pos_stride", _c_i64)]
+
+
+_PV = ctypes.POINTER(PomView)
+_PR = ctypes.POINTER(PomRope)
+
+SIGNATURES = {
+    "pom_abi_version": (_c_int, []),
+    "pom_last_error": (ctypes.c_char_p, []),
+    "pom_agg_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int]),
+    "pom_agg_fwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64, _c_i64,
+                             _c_i64, _c_vp, _c_i64, _PR, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "pom_agg_bwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64, _c_i64,
+                             _c_vp, _c_i64, _c_i64, _PR, _c_vp, _PV, _c_vp, _c_vp, _c_size, _c_vp]),
+    "pom_gate_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
+    "pom_gate_fwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR, _PV, _c_vp]),
+    "pom_gate_bwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR, _PV, _PV,
+                              _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_lib_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load libpom_amd.so (once) and bind every declared symbol; raise if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"pom_amd: HIP library not found at {LIB_PATH}; build it with "
+                "`python pom_amd/csrc/build.py` (there is no CPU fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.pom_abi_version() != 1:
+            raise RuntimeError("pom_amd: ABI version mismatch; rebuild libpom_amd.so")
+        _lib = lib
+    return _lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False
+
+
+def check(rc: int, what: str) -> None:
+    """Map a pom_status to a Python exception carrying pom_last_error()."""
+    if rc == POM_OK:
+        return
+    msg = f"{what}: {load().pom_last_error().decode(errors='replace')}"
+    if rc == POM_ERR_INVALID:
+        raise ValueError(msg)
+    if rc == POM_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise TypeError(f"pom_amd: unsupported dtype {t.dtype}; expected float32, bfloat16 or float16")
+
+
+def require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("pom_amd runs on ROCm devices only (got a CPU tensor); "
+                               "move the module and inputs to a GPU")
+
+
+def view3(t: torch.Tensor) -> PomView:
+    """(B, N, C) tensor with unit last-axis stride -> PomView."""
+    if t.dim() != 3:
+        raise ValueError(f"expected a 3-D (B, N, C) tensor, got shape {tuple(t.shape)}")
+    if t.shape[2] > 1 and t.stride(2) != 1:
+        raise ValueError("the channel axis must have unit stride")
+    return PomView(t.data_ptr(), t.stride(0), t.stride(1))
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+_ws_cache: dict = {}
+_ws_lock = threading.Lock()
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-initialised workspace for one (device, stream).
+
+    The library leaves the counter prefix zero after every successful call, so
+    the buffer is reused across calls on the same stream; a larger request
+    allocates a new zeroed buffer (stream-ordered, so the old one may still be
+    in use by queued kernels until the allocator recycles it).
+    """
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    with _ws_lock:
+        buf = _ws_cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, COUNTER_BYTES + (4 << 20))
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            _ws_cache[key] = buf
+        return buf
+
+
+class RopeSpec:
+    """Device-side RoPE description: fp32 tables and int64 positions kept alive
+    for as long as the kernels may read them."""
+
+    def __init__(self, kind: int, tables, pos: torch.Tensor):
+        self.kind = kind
+        self.tables = [t.float().contiguous() for t in tables]
+        self.pos = pos.to(torch.int64).contiguous()
+        width = self.tables[0].shape[1]
+        for t in self.tables:
+            if t.shape[1] != width:
+                raise ValueError("RoPE tables must share their width")
+        self.width = width
+
+    def struct(self) -> PomRope:
+        t = self.tables
+        if self.kind == ROPE_1D:
+            return PomRope(ROPE_1D, t[0].data_ptr(), t[1].data_ptr(), None, None, t[0].stride(0),
+                           t[0].shape[0], 0, self.pos.data_ptr(), 1)
+        return PomRope(ROPE_2D, t[0].data_ptr(), t[1].data_ptr(), t[2].data_ptr(), t[3].data_ptr(),
+                       t[0].stride(0), t[0].shape[0], t[2].shape[0], self.pos.data_ptr(), 2)
+
+
+def rope_ptr(spec: Optional[RopeSpec]):
+    return None if spec is None else ctypes.byref(spec.struct())

@@ -1,0 +1,63 @@
+// Lane -> channel mapping shared by the aggregation and gating kernels.
+//
+// Plain mode: a lane owns CPT consecutive channels [vcol*CPT, vcol*CPT+CPT).
+// RoPE modes: a lane owns CPT consecutive rotation pairs; slot i < CPT is the
+// first channel of pair i, slot CPT+i its partner.
+//   1-D (pom/pom_rope.py:152-180): pair j = (j, j + P/2), table column j.
+//   2-D (pom/pom_rope.py:183-235): q = P/4; pair j < q = (j, j+q) on the row
+//        tables, pair j >= q = (2q + j', 3q + j'), j' = j - q, on the column
+//        tables.
+#pragma once
+#include "common.h"
+#include "pom_internal.h"
+
+namespace pom {
+
+// Channel mapping for one lane: slot i in [0, CPT2) -> channel index.
+template <int CPT, int MODE>
+struct LaneMap {
+  static constexpr int CPT2 = (MODE == MODE_ROPE1D || MODE == MODE_ROPE2D) ? 2 * CPT : CPT;
+  int64_t c1 = 0, c2 = 0, tcol = 0;
+  int table = 0;   // 0 = row / 1-D tables, 1 = column tables (2-D)
+
+  __device__ __forceinline__ void init(int64_t vcol, int64_t P) {
+    if constexpr (MODE == MODE_ROPE1D) {
+      const int64_t j = vcol * CPT;
+      c1 = j; c2 = j + P / 2; tcol = j;
+    } else if constexpr (MODE == MODE_ROPE2D) {
+      const int64_t q = P / 4, j = vcol * CPT;
+      if (j < q) { c1 = j; c2 = j + q; tcol = j; table = 0; }
+      else { const int64_t jj = j - q; c1 = 2 * q + jj; c2 = 3 * q + jj; tcol = jj; table = 1; }
+    } else {
+      c1 = vcol * CPT;
+    }
+  }
+  __device__ __forceinline__ int64_t chan(int i) const {
+    if constexpr (CPT2 == CPT) return c1 + i;
+    else return i < CPT ? c1 + i : c2 + (i - CPT);
+  }
+};
+
+// Slot s of the partial buffers -> channel (same mapping as LaneMap).
+template <int CPT, int MODE>
+__device__ __forceinline__ int64_t slot_chan(int64_t s, int64_t P) {
+  constexpr int CPT2 = LaneMap<CPT, MODE>::CPT2;
+  LaneMap<CPT, MODE> m;
+  m.init(s / CPT2, P);
+  return m.chan((int)(s % CPT2));
+}
+
+// cos/sin of token n for CPT consecutive rotation pairs starting at table column
+// tcol.  Positions outside the table are clamped so a bad position can never
+// read outside the table.
+template <int CPT>
+__device__ __forceinline__ void load_table(const RopeTables& t, int table, int64_t n, int64_t tcol,
+                                           float (&cs)[CPT], float (&sn)[CPT]) {
+  int64_t pos = t.pos[n * t.pos_sn + table];
+  const int64_t rows = table ? t.rows1 : t.rows0;
+  pos = pos < 0 ? 0 : (pos >= rows ? rows - 1 : pos);
+  load_f32<CPT>((table ? t.cos1 : t.cos0) + pos * t.stride + tcol, cs);
+  load_f32<CPT>((table ? t.sin1 : t.sin0) + pos * t.stride + tcol, sn);
+}
+
+}  // namespace pom

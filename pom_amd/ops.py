@@ -1,0 +1,353 @@
+"""Autograd operators over the HIP kernels (C ABI in include/pom_amd.h).
+
+Kernel-level entry points mirror the reference's Triton entry points, same
+arguments, return shapes and dtypes:
+
+  poly_agg_mean_hip(x, coeff, k)             ~ poly_agg_mean_triton        pom/pom_triton.py:383-403
+  poly_agg_masked_hip(x, mask, coeff, k)     ~ poly_agg_masked_triton      pom/pom_triton_masked.py:402-428
+  poly_agg_causal_hip(x, coeff, k)           ~ poly_agg_causal_triton      pom/pom_triton_causal.py:400-423
+  poly_agg_rope_mean_hip(x, coeff, k, fc, fs, positions)
+                                             ~ poly_agg_rope_mean_triton   pom/pom_triton_rope.py:985-1017
+  poly_agg_rope_causal_hip(...)              ~ poly_agg_rope_causal_triton pom/pom_triton_rope.py:1020-1053
+  poly_agg_block_causal_hip(x, coeff, k, frame_len)   frame-causal mean, compact (B, N/L, P)
+
+and the fused layer operator ``pom_layer`` (projection GEMMs + aggregation +
+gating) used by the modules.  Inputs are borrowed, never copied: the
+aggregation reads a strided view (e.g. the h-half of the fused projection)
+and its backward writes grad_x straight into the matching half of dY.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import RopeSpec, check, dtype_code, ptr, rope_ptr, view3, workspace, stream_handle
+
+
+def _check_degree(k: int) -> None:
+    if k > _lib.MAX_DEGREE:
+        raise NotImplementedError(f"pom_amd kernels support degree k <= {_lib.MAX_DEGREE} (got {k})")
+    if k < 1:
+        raise ValueError(f"degree must be >= 1 (got {k})")
+
+
+def _coeff32(coeff: torch.Tensor, p: int, k: int) -> torch.Tensor:
+    if coeff.shape != (p, k):
+        raise ValueError(f"coeff must have shape ({p}, {k}), got {tuple(coeff.shape)}")
+    return coeff.detach().float().contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Raw launches (no autograd)
+# ---------------------------------------------------------------------------
+
+def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
+                mask32: Optional[torch.Tensor] = None, carry: Optional[torch.Tensor] = None,
+                n_past: int = 0, rope: Optional[RopeSpec] = None):
+    """Launch pom_agg_fwd.  Returns (out (B, N/frame_len, P) x.dtype, count or None)."""
+    lib = _lib.load()
+    B, N, P = x.shape
+    dt = dtype_code(x)
+    out = torch.empty(B, N // frame_len, P, dtype=x.dtype, device=x.device)
+    count = torch.empty(B, dtype=torch.float32, device=x.device) if mask32 is not None else None
+    rk = rope.kind if rope is not None else _lib.ROPE_NONE
+    nbytes = lib.pom_agg_workspace_size(dt, B, N, P, k, frame_len, rk, 0)
+    if nbytes == 0:
+        nbytes = _lib.COUNTER_BYTES   # invalid shape: the launch below reports why
+    ws = workspace(x.device, nbytes)
+    xv = view3(x)
+    if carry is not None:
+        carry = carry.reshape(B, P).contiguous()
+        if carry.dtype != x.dtype:
+            carry = carry.to(x.dtype)
+    rc = lib.pom_agg_fwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+                         mask32.stride(0) if mask32 is not None else 0,
+                         mask32.stride(1) if mask32 is not None else 0,
+                         frame_len, ptr(carry), n_past, rope_ptr(rope), out.data_ptr(), ptr(count),
+                         ws.data_ptr(), ws.numel(), stream_handle(x.device))
+    check(rc, "pom_agg_fwd")
+    return out, count
+
+
+def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int, go32: torch.Tensor,
+                 grad_x: torch.Tensor, mask32: Optional[torch.Tensor] = None,
+                 count: Optional[torch.Tensor] = None, n_past: int = 0,
+                 rope: Optional[RopeSpec] = None) -> torch.Tensor:
+    """Launch pom_agg_bwd; writes grad_x in place and returns grad_coeff (P, K) fp32."""
+    lib = _lib.load()
+    B, N, P = x.shape
+    dt = dtype_code(x)
+    gc = torch.empty(P, k, dtype=torch.float32, device=x.device)
+    rk = rope.kind if rope is not None else _lib.ROPE_NONE
+    nbytes = lib.pom_agg_workspace_size(dt, B, N, P, k, frame_len, rk, 1) or _lib.COUNTER_BYTES
+    ws = workspace(x.device, nbytes)
+    xv, gv = view3(x), view3(grad_x)
+    go32 = go32.contiguous()
+    rc = lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+                         mask32.stride(0) if mask32 is not None else 0,
+                         mask32.stride(1) if mask32 is not None else 0, ptr(count),
+                         frame_len, n_past, rope_ptr(rope), go32.data_ptr(), ctypes.byref(gv),
+                         gc.data_ptr(), ws.data_ptr(), ws.numel(), stream_handle(x.device))
+    check(rc, "pom_agg_bwd")
+    return gc
+
+
+def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg32: torch.Tensor,
+                 rope: Optional[RopeSpec] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sh = R hardsigmoid(ys + bias) * hagg[group], via pom_gate_fwd."""
+    lib = _lib.load()
+    B, N, P = ys.shape
+    G = hagg32.shape[1]
+    sh = torch.empty(B, N, P, dtype=ys.dtype, device=ys.device) if out is None else out
+    yv, sv = view3(ys), view3(sh)
+    rc = lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G,
+                          rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
+    check(rc, "pom_gate_fwd")
+    return sh
+
+
+def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg32: torch.Tensor,
+                  grad_sh: torch.Tensor, grad_ys: torch.Tensor, rope: Optional[RopeSpec] = None,
+                  want_bias: bool = True):
+    """Writes grad_ys in place; returns (grad_hagg (B, G, P) fp32, grad_bias (P,) fp32 or None)."""
+    lib = _lib.load()
+    B, N, P = ys.shape
+    G = hagg32.shape[1]
+    dt = dtype_code(ys)
+    gh = torch.empty(B, G, P, dtype=torch.float32, device=ys.device)
+    gb = torch.empty(P, dtype=torch.float32, device=ys.device) if want_bias else None
+    rk = rope.kind if rope is not None else _lib.ROPE_NONE
+    nbytes = lib.pom_gate_workspace_size(dt, B, N, P, G, rk) or _lib.COUNTER_BYTES
+    ws = workspace(ys.device, nbytes)
+    yv, gv, dv = view3(ys), view3(grad_sh), view3(grad_ys)
+    rc = lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G, rope_ptr(rope),
+                          ctypes.byref(gv), ctypes.byref(dv), gh.data_ptr(), ptr(gb), ws.data_ptr(),
+                          ws.numel(), stream_handle(ys.device))
+    check(rc, "pom_gate_bwd")
+    return gh, gb
+
+
+# ---------------------------------------------------------------------------
+# Kernel-level autograd operators (drop-ins for the Triton entry points)
+# ---------------------------------------------------------------------------
+
+class _PolyAgg(torch.autograd.Function):
+    """Aggregation with every mode of pom_agg_fwd / pom_agg_bwd."""
+
+    @staticmethod
+    def forward(ctx, x, coeff, k, frame_len, mask32, rope, carry, n_past):
+        _lib.require_device(x)
+        B, N, P = x.shape
+        c32 = _coeff32(coeff, P, k)
+        out, count = agg_forward(x, c32, k, frame_len, mask32, carry, n_past, rope)
+        ctx.save_for_backward(x, c32, mask32, count)
+        ctx.k, ctx.frame_len, ctx.rope, ctx.n_past = k, frame_len, rope, n_past
+        ctx.coeff_dtype = coeff.dtype
+        ctx.has_carry = carry is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, c32, mask32, count = ctx.saved_tensors
+        go32 = grad_out.float().contiguous()
+        gx = torch.empty_like(x, memory_format=torch.contiguous_format)
+        gc = agg_backward(x, c32, ctx.k, ctx.frame_len, go32, gx, mask32, count, ctx.n_past, ctx.rope)
+        g_carry = None
+        if ctx.has_carry and ctx.needs_input_grad[6]:
+            nf = go32.shape[1]
+            w = ctx.n_past / (ctx.n_past + torch.arange(nf, device=x.device, dtype=torch.float32) + 1.0)
+            g_carry = (go32 * w.view(1, nf, 1)).sum(dim=1, keepdim=True).to(x.dtype)
+        return gx, gc.to(ctx.coeff_dtype), None, None, None, None, g_carry, None
+
+
+def _mask32(mask: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    B, N, _ = x.shape
+    if mask.shape != (B, N):
+        raise ValueError(f"mask must have shape ({B}, {N}), got {tuple(mask.shape)}")
+    return mask.to(device=x.device, dtype=torch.float32).contiguous()
+
+
+def poly_agg_mean_hip(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
+    """(B, N, D) -> (B, 1, D) mean of p(act(x)) in x.dtype."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, x.shape[1], None, None, None, 0)
+
+
+def poly_agg_masked_hip(x: torch.Tensor, mask: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
+    """(B, N, D), (B, N) weights -> (B, 1, D) weighted mean (all-zero row -> 0)."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, x.shape[1], _mask32(mask, x), None, None, 0)
+
+
+def poly_agg_block_causal_hip(x: torch.Tensor, coeff: torch.Tensor, k: int, frame_len: int) -> torch.Tensor:
+    """(B, N, D) -> (B, N/frame_len, D): row f = mean over frames 0..f."""
+    _check_degree(k)
+    if frame_len <= 0 or x.shape[1] % frame_len:
+        raise ValueError(f"frame_len {frame_len} must divide the sequence length {x.shape[1]}")
+    return _PolyAgg.apply(x, coeff, k, frame_len, None, None, None, 0)
+
+
+def poly_agg_causal_hip(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
+    """(B, N, D) -> (B, N, D) token-causal prefix mean."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, 1, None, None, None, 0)
+
+
+def _rope1d(x: torch.Tensor, freqs_cos, freqs_sin, positions) -> RopeSpec:
+    B, N, D = x.shape
+    if D % 2 != 0:
+        raise ValueError(f"D must be even for RoPE (got {D})")
+    if positions is None:
+        positions = torch.arange(N, device=x.device, dtype=torch.int64)
+    if freqs_cos.shape[1] < D // 2:
+        raise ValueError("RoPE tables are narrower than D/2")
+    return RopeSpec(_lib.ROPE_1D, [freqs_cos, freqs_sin], positions.to(x.device))
+
+
+def poly_agg_rope_mean_hip(x, coeff, k, freqs_cos, freqs_sin, positions=None):
+    """Fused act + poly + 1-D RoPE + mean: (B, N, D) -> (B, 1, D)."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, x.shape[1], None, _rope1d(x, freqs_cos, freqs_sin, positions), None, 0)
+
+
+def poly_agg_rope_causal_hip(x, coeff, k, freqs_cos, freqs_sin, positions=None):
+    """Fused act + poly + 1-D RoPE + causal prefix mean: (B, N, D) -> (B, N, D)."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, 1, None, _rope1d(x, freqs_cos, freqs_sin, positions), None, 0)
+
+
+def poly_agg_rope_hip(x, coeff, k, rope: RopeSpec, frame_len: Optional[int] = None):
+    """Aggregation of rotated features for an arbitrary RopeSpec (1-D or 2-D)."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, x.shape[1] if frame_len is None else frame_len, None, rope, None, 0)
+
+
+def poly_agg_state_hip(x, coeff, k, carry: Optional[torch.Tensor], n_past: int) -> torch.Tensor:
+    """One PoM.state_forward aggregation step: (n_past*carry + mean)/(n_past+1)."""
+    _check_degree(k)
+    return _PolyAgg.apply(x, coeff, k, x.shape[1], None, None, carry, n_past if carry is not None else 0)
+
+
+class _Gate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ys, bias, hagg, rope):
+        _lib.require_device(ys, hagg)
+        B, N, P = ys.shape
+        b32 = None if bias is None else bias.detach().float().contiguous()
+        h32 = hagg.detach().float().contiguous()
+        sh = gate_forward(ys, b32, h32, rope)
+        ctx.save_for_backward(ys, b32, h32)
+        ctx.rope = rope
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        ctx.hagg_dtype = hagg.dtype
+        return sh
+
+    @staticmethod
+    def backward(ctx, grad_sh):
+        ys, b32, h32 = ctx.saved_tensors
+        gys = torch.empty_like(ys, memory_format=torch.contiguous_format)
+        gh, gb = gate_backward(ys, b32, h32, grad_sh, gys, ctx.rope, want_bias=b32 is not None)
+        return (gys, None if gb is None else gb.to(ctx.bias_dtype), gh.to(ctx.hagg_dtype), None)
+
+
+def gate_hip(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor,
+             rope: Optional[RopeSpec] = None) -> torch.Tensor:
+    """R(pos) hardsigmoid(ys + bias) * hagg, hagg (B, G, P) broadcast over N/G tokens per group."""
+    return _Gate.apply(ys, bias, hagg, rope)
+
+
+# ---------------------------------------------------------------------------
+# Fused PoM layer: qc_proj GEMM -> aggregation -> gating -> ag_proj GEMM
+# ---------------------------------------------------------------------------
+
+class _PoMLayer(torch.autograd.Function):
+    """Self-mixing PoM layer (n_groups == 1, n_sel_heads <= 1) — pom/pom.py:216-231
+    composed with _get_h_s (:204-207), pom() (:125-135) and, for RoPE,
+    pom/pom_rope.py:476-526.
+
+    Memory plan (T = B*N tokens):
+      forward : Y = x W_qc^T (T, 2P) -> hagg (B, G, P) -> sh (T, P) -> out (T, D)
+      backward: dsh = g W_ag (T, P); dY (T, 2P) is filled in two halves by the
+                gate (s-half) and aggregation (h-half) kernels, then
+                dx = dY W_qc and dW_qc = dY^T x.
+    Saved: x, Y, sh, hagg (fp32), the fp32 coefficient/bias copies.
+    Returns (out, hagg) — hagg in x.dtype, differentiable (state_forward's carry).
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, mask, rope_h, rope_s, carry, n_past):
+        _lib.require_device(x)
+        B, N, D = x.shape
+        P = coeff.shape[0]
+        dt = x.dtype
+        x2 = x.reshape(B * N, D)
+        wq = w_qc if w_qc.dtype == dt else w_qc.to(dt)
+        y = torch.mm(x2, wq.t())                                    # (T, 2P)
+        y3 = y.view(B, N, 2 * P)
+        h_view, s_view = y3[..., :P], y3[..., P:]
+        c32 = _coeff32(coeff, P, k)
+        hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
+        h32 = hagg.float()
+        b32 = se_bias.detach().float().contiguous()
+        sh = gate_forward(s_view, b32, h32, rope_s)                 # (B, N, P)
+        wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
+        out = torch.mm(sh.view(B * N, P), wa.t())
+        if b_ag is not None:
+            out = out + b_ag.to(dt)
+        ctx.save_for_backward(x, y, sh, h32, c32, b32, wq, wa, mask, count)
+        ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None)
+        ctx.dtypes = (w_qc.dtype, se_bias.dtype, coeff.dtype, w_ag.dtype,
+                      None if b_ag is None else b_ag.dtype)
+        return out.view(B, N, D), hagg
+
+    @staticmethod
+    def backward(ctx, grad_out, grad_hagg):
+        x, y, sh, h32, c32, b32, wq, wa, mask, count = ctx.saved_tensors
+        k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias = ctx.meta
+        B, N, D = x.shape
+        P = c32.shape[0]
+        T = B * N
+        dt = x.dtype
+        g2 = grad_out.reshape(T, D)
+        if g2.dtype != dt:
+            g2 = g2.to(dt)
+        dsh = torch.mm(g2, wa)                                      # (T, P)
+        dw_ag = torch.mm(g2.t(), sh.view(T, P))                     # (D, P)
+        db_ag = g2.float().sum(0) if has_bias else None
+        y3 = y.view(B, N, 2 * P)
+        dy = torch.empty(T, 2 * P, dtype=dt, device=x.device)
+        dy3 = dy.view(B, N, 2 * P)
+        dh, dbias = gate_backward(y3[..., P:], b32, h32, dsh.view(B, N, P), dy3[..., P:], rope_s)
+        if grad_hagg is not None:
+            dh = dh + grad_hagg.float()
+        dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h)
+        dx = torch.mm(dy, wq)                                       # (T, D)
+        dw_qc = torch.mm(dy.t(), x.reshape(T, D))                   # (2P, D)
+        g_carry = None
+        if has_carry:
+            nf = dh.shape[1]
+            w = n_past / (n_past + torch.arange(nf, device=x.device, dtype=torch.float32) + 1.0)
+            g_carry = (dh * w.view(1, nf, 1)).sum(dim=1, keepdim=True).to(dt)
+        tq, tb, tc, ta, tab = ctx.dtypes
+        return (dx.view(B, N, D), dw_qc.to(tq), dbias.to(tb), dcoeff.to(tc), dw_ag.to(ta),
+                None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None)
+
+
+def pom_layer(x, w_qc, se_bias, coeff, w_ag, b_ag, k: int, frame_len: Optional[int] = None,
+              mask: Optional[torch.Tensor] = None, rope_h: Optional[RopeSpec] = None,
+              rope_s: Optional[RopeSpec] = None, carry: Optional[torch.Tensor] = None,
+              n_past: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Run the fused layer; returns (out (B, N, D), hagg (B, G, P))."""
+    _check_degree(k)
+    if not x.is_contiguous():
+        x = x.contiguous()
+    B, N, _ = x.shape
+    frame_len = N if frame_len is None else frame_len
+    if frame_len <= 0 or N % frame_len:
+        raise ValueError(f"frame_len {frame_len} must divide the sequence length {N}")
+    m32 = None if mask is None else _mask32(mask, x)
+    return _PoMLayer.apply(x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, m32, rope_h, rope_s,
+                           carry, n_past if carry is not None else 0)
