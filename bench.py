@@ -1,0 +1,331 @@
+"""PoM layer benchmark on one MI355X: forward + backward tokens/s, per-kernel
+roofline fractions and a CPU baseline, printed as ONE JSON line.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
+                  [--no-cpu] [--fwd] [--copy-calib MiB]
+
+A step is one forward + backward of one PoM layer over one batch of synthetic
+input that is resident in HBM before the timed region starts (x, upstream
+gradient and weights).  The default workload is config 2 of the baseline
+(image-DiT layer: B=16, N=1024, D=1152, degree 2, expand 2, bf16).  Every
+launch of the layer (six projection GEMMs, aggregation and gating kernels) is
+bracketed by HIP events on the launch stream inside the timed region, giving
+each kernel's average duration; the roofline object reports the kernel that
+takes the most time per step, and "kernels" reports all of them.
+
+The CPU baseline runs the oracle (a pure-PyTorch restatement of the reference
+path) in fp32 on the host cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "PoM layer fwd+bwd tokens/sec at B=16,N=1024,D=1152 bf16; % HBM/MFMA roofline"
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+MFMA_BF16_PEAK = 2.5e15    # FLOP/s, MI355X dense bf16
+
+# name: (B, N, D, degree, expand, variant, extra)
+CONFIGS = {
+    "c2": dict(B=16, N=1024, D=1152, K=2, E=2, variant="mean",
+               workload="C2 image-DiT PoM layer fwd+bwd (B=16, N=1024, D=1152, degree=2, expand=2)"),
+    "c3": dict(B=32, N=2048, D=1024, K=3, E=2, variant="masked",
+               workload="C3 masked PoM layer fwd+bwd (B=32, N=2048, D=1024, degree=3, expand=2, "
+                        "valid length U[256,2048])"),
+    "c4": dict(B=4, N=16384, D=1024, K=2, E=4, variant="block", frame_len=1024,
+               workload="C4 block-causal video PoM layer fwd+bwd (B=4, 16 frames x 1024, D=1024, "
+                        "degree=2, expand=4)"),
+    "c5": dict(B=8, N=4096, D=1536, K=2, E=2, variant="rope2d", H=64, W=64,
+               workload="C5 2-D RoPE PoM layer fwd+bwd (B=8, N=4096 on 64x64, D=1536, degree=2, expand=2)"),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    ap.add_argument("--no-kernel-timing", action="store_true",
+                    help="time the steps without per-launch events")
+    ap.add_argument("--copy-calib", type=float, default=0.0,
+                    help="instead of the layer, run a plain device copy of this many MiB "
+                         "(calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# Workload construction (identical seeded inputs for the GPU and CPU legs)
+# ---------------------------------------------------------------------------
+
+def make_inputs(cfg):
+    import torch
+    g1 = torch.Generator().manual_seed(1)
+    g2 = torch.Generator().manual_seed(2)
+    x = torch.randn(cfg["B"], cfg["N"], cfg["D"], generator=g1)
+    go = torch.randn(cfg["B"], cfg["N"], cfg["D"], generator=g2)
+    extra = {}
+    if cfg["variant"] == "masked":
+        g3 = torch.Generator().manual_seed(3)
+        lens = torch.randint(256, cfg["N"] + 1, (cfg["B"],), generator=g3)
+        extra["mask"] = torch.arange(cfg["N"]).view(1, -1) < lens.view(-1, 1)
+        extra["lens"] = lens
+    if cfg["variant"] == "rope2d":
+        H, W = cfg["H"], cfg["W"]
+        extra["positions_hw"] = torch.stack(torch.meshgrid(torch.arange(H), torch.arange(W), indexing="ij"),
+                                            -1).reshape(-1, 2)
+    return x, go, extra
+
+
+def make_module(cfg):
+    import torch
+    import pom_amd
+    torch.manual_seed(0)
+    if cfg["variant"] == "rope2d":
+        return pom_amd.PoMRoPE(cfg["D"], cfg["K"], cfg["E"], 1, 1, False, max_h=cfg["H"], max_w=cfg["W"],
+                               rope_2d=True)
+    return pom_amd.PoM(cfg["D"], cfg["K"], cfg["E"], 1, 1, False)
+
+
+def forward_fn(cfg, extra_dev):
+    import pom_amd
+    v = cfg["variant"]
+    if v == "mean":
+        return lambda m, x: m(x)
+    if v == "masked":
+        return lambda m, x: m(x, mask=extra_dev["mask"])
+    if v == "block":
+        desc = pom_amd.block_causal(cfg["frame_len"])
+        return lambda m, x: m(x, mask=desc)
+    if v == "rope2d":
+        return lambda m, x: m(x, positions_hw=extra_dev["positions_hw"])
+    raise ValueError(v)
+
+
+# ---------------------------------------------------------------------------
+# Algorithmic work per kernel launch
+# ---------------------------------------------------------------------------
+
+def kernel_work(cfg, extra):
+    """name -> (bound, algorithmic bytes or flops per launch, what one unit is)."""
+    B, N, D, K, E = cfg["B"], cfg["N"], cfg["D"], cfg["K"], cfg["E"]
+    T, P, e = B * N, E * D, 2
+    G = {"mean": 1, "masked": 1, "block": N // cfg.get("frame_len", N), "rope2d": 1}[cfg["variant"]]
+    read_tok = T
+    if cfg["variant"] == "masked":
+        read_tok = int(extra["lens"].sum())
+    agg_out = B * G * P * e
+    rope_tab = 0
+    if cfg["variant"] == "rope2d":
+        rope_tab = 0   # tables are (64, P/4) fp32: cache resident, not counted
+    mask_b = B * N * 4 if cfg["variant"] == "masked" else 0
+    w = {
+        "gemm_qc_fwd": ("mfma", 2.0 * T * D * 2 * P),
+        "gemm_ag_fwd": ("mfma", 2.0 * T * P * D),
+        "gemm_ag_dgrad": ("mfma", 2.0 * T * D * P),
+        "gemm_ag_wgrad": ("mfma", 2.0 * T * D * P),
+        "gemm_qc_dgrad": ("mfma", 2.0 * T * 2 * P * D),
+        "gemm_qc_wgrad": ("mfma", 2.0 * T * 2 * P * D),
+        # x read (valid tokens only when masked) + aggregate written
+        "agg_fwd": ("hbm", float(read_tok * P * e + agg_out + mask_b + rope_tab)),
+        # x read for valid tokens, grad_x written for every token, fp32 upstream grad read
+        "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + B * G * P * 4 + mask_b)),
+        # y_s read, sh written
+        "gate_fwd": ("hbm", float(2 * T * P * e + B * G * P * 4)),
+        # y_s and dsh read, dy_s written
+        "gate_bwd": ("hbm", float(3 * T * P * e + B * G * P * 4)),
+    }
+    return w
+
+
+# ---------------------------------------------------------------------------
+# GPU leg
+# ---------------------------------------------------------------------------
+
+def gpu_run(cfg, steps, warmup, kernel_timing):
+    import torch
+    from pom_amd import ops, _lib
+    _lib.load()
+    dev = torch.device("cuda:0")
+    x, go, extra = make_inputs(cfg)
+    m = make_module(cfg).to(dev, torch.bfloat16)
+    xd = x.to(dev, torch.bfloat16).requires_grad_(True)
+    god = go.to(dev, torch.bfloat16)
+    extra_dev = {k: v.to(dev) for k, v in extra.items()}
+    fwd = forward_fn(cfg, extra_dev)
+    params = list(m.parameters())
+
+    def step():
+        for p in params:
+            p.grad = None
+        xd.grad = None
+        out = fwd(m, xd)
+        out.backward(god)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K fwd+bwd steps
+    ops.kernel_timer = [] if kernel_timing else None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    spans = ops.kernel_timer or []
+    ops.kernel_timer = None
+    per = {}
+    for name, s, e in spans:
+        per.setdefault(name, []).append(s.elapsed_time(e) * 1e-3)   # seconds
+    ms_step = (t1 - t0) / steps * 1e3
+
+    # forward-only throughput (no autograd graph)
+    with torch.no_grad():
+        for _ in range(max(2, warmup // 2)):
+            fwd(m, xd)
+        torch.cuda.synchronize()
+        f0 = time.perf_counter()
+        for _ in range(steps):
+            fwd(m, xd)
+        torch.cuda.synchronize()
+        f1 = time.perf_counter()
+    ms_fwd = (f1 - f0) / steps * 1e3
+    return ms_step, ms_fwd, per, extra
+
+
+def copy_calib(mib: float):
+    """A plain device-to-device copy of known size, for counter calibration."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = int(mib * (1 << 20)) // 2
+    a = torch.randn(n, device=dev).to(torch.bfloat16)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calib_bytes_read": n * 2, "copy_calib_bytes_written": n * 2, "launches": 10}))
+
+
+# ---------------------------------------------------------------------------
+# CPU leg: the oracle, fp32, on the host cores
+# ---------------------------------------------------------------------------
+
+def cpu_run(cfg, budget_s: float):
+    import torch
+    from oracle import pom_oracle as O
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    x, go, extra = make_inputs(cfg)
+    torch.manual_seed(0)
+    rope2d = True if cfg["variant"] == "rope2d" else None
+    prm = O.init_params(cfg["D"], cfg["K"], cfg["E"], rope_2d=rope2d,
+                        max_h=cfg.get("H", 64), max_w=cfg.get("W", 64))
+    for t in (prm.w_qc, prm.se_bias, prm.po_coeff, prm.w_ag):
+        t.requires_grad_(True)
+    # bounded sample: the first batch rows of the workload, as many as the budget allows
+    v = cfg["variant"]
+
+    def run(nb):
+        xs = x[:nb].clone().requires_grad_(True)
+        if v == "mean":
+            out = O.pom_forward(prm, xs)
+        elif v == "masked":
+            out = O.pom_forward(prm, xs, mask=extra["mask"][:nb])
+        elif v == "block":
+            out = O.pom_forward(prm, xs, mask=("block_causal", cfg["frame_len"]))
+        else:
+            out = O.rope_forward(prm, xs, positions_hw=extra["positions_hw"])
+        out.backward(go[:nb])
+
+    nb = 1
+    t0 = time.perf_counter()
+    run(nb)                                  # warm-up on one batch row
+    t_one = time.perf_counter() - t0
+    nb = max(1, min(cfg["B"], int(budget_s / 3 / max(t_one, 1e-3))))
+    times = []
+    for _ in range(3):
+        s = time.perf_counter()
+        run(nb)
+        times.append(time.perf_counter() - s)
+    times.sort()
+    med = times[1]
+    tok = nb * cfg["N"]
+    return {"value": tok / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"oracle fp32 layer fwd+bwd on {nb} of {cfg['B']} batch rows ({tok} tokens), "
+                      f"median of 3 after 1 warm-up, torch.set_num_threads({cores})"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {a.gpus}); "
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+        sys.exit(2)
+    if a.copy_calib > 0:
+        copy_calib(a.copy_calib)
+        return
+    cfg = CONFIGS[a.config]
+    ms_step, ms_fwd, per, extra = gpu_run(cfg, a.steps, a.warmup, not a.no_kernel_timing)
+    T = cfg["B"] * cfg["N"]
+    work = kernel_work(cfg, extra)
+    kernels = {}
+    for name, durs in per.items():
+        bound, amount = work[name]
+        avg = sum(durs) / len(durs)
+        per_step = sum(durs) / a.steps
+        peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
+        achieved = amount / avg
+        kernels[name] = {"bound": bound, "avg_us": round(avg * 1e6, 2), "us_per_step": round(per_step * 1e6, 2),
+                         "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
+                         "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4),
+                         "launches_per_step": len(durs) / a.steps}
+    roofline = None
+    if kernels:
+        dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
+        k = kernels[dom]
+        roofline = {"kernel": dom, "bound": k["bound"], "achieved": k["achieved"],
+                    "peak": 8000.0 if k["bound"] == "hbm" else 2500.0, "unit": k["unit"], "frac": k["frac"],
+                    "traffic": None}
+    res = {
+        "metric": METRIC, "value": round(T / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: x~N(0,1) seed 1, upstream grad~N(0,1) seed 2, weights nn.Linear init seed 0",
+        "config": {"workload": cfg["workload"], "B": cfg["B"], "N": cfg["N"], "D": cfg["D"], "degree": cfg["K"],
+                   "expand": cfg["E"], "tokens_per_step": T},
+        "fwd_tokens_per_s": round(T / (ms_fwd * 1e-3), 1), "ms_fwd": round(ms_fwd, 4),
+        "roofline": roofline, "kernels": kernels,
+    }
+    if kernels:
+        agg = [n for n in ("agg_fwd", "agg_bwd", "gate_fwd", "gate_bwd") if n in kernels]
+        gem = [n for n in kernels if n.startswith("gemm")]
+        t_hbm = sum(kernels[n]["us_per_step"] for n in agg)
+        t_mf = sum(kernels[n]["us_per_step"] for n in gem)
+        b_hbm = sum(work[n][1] for n in agg)
+        f_mf = sum(work[n][1] for n in gem)
+        res["roofline_groups"] = {
+            "hip_streaming_kernels": {"us_per_step": round(t_hbm, 2),
+                                      "frac_hbm": round(b_hbm / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None},
+            "projection_gemms": {"us_per_step": round(t_mf, 2),
+                                 "frac_mfma": round(f_mf / (t_mf * 1e-6) / MFMA_BF16_PEAK, 4) if t_mf else None},
+            "ideal_step_us": round((b_hbm / HBM_PEAK + f_mf / MFMA_BF16_PEAK) * 1e6, 2),
+        }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_run(cfg, a.cpu_seconds)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -27,6 +27,32 @@ from . import _lib
 from ._lib import RopeSpec, check, dtype_code, ptr, rope_ptr, view3, workspace, stream_handle
 
 
+# Optional per-launch timing: when ``kernel_timer`` is a list, every launch
+# site below appends (name, start_event, end_event) recorded on the stream the
+# launch goes to.  bench.py uses it to time each kernel inside its timed region.
+kernel_timer: Optional[list] = None
+
+
+class _Span:
+    __slots__ = ("name", "ev")
+
+    def __init__(self, name: str):
+        self.name = name
+        self.ev = None
+
+    def __enter__(self):
+        if kernel_timer is not None:
+            self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            self.ev[0].record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.ev is not None:
+            self.ev[1].record()
+            kernel_timer.append((self.name, self.ev[0], self.ev[1]))
+        return False
+
+
 def _check_degree(k: int) -> None:
     if k > _lib.MAX_DEGREE:
         raise NotImplementedError(f"pom_amd kernels support degree k <= {_lib.MAX_DEGREE} (got {k})")
@@ -63,11 +89,12 @@ def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
         carry = carry.reshape(B, P).contiguous()
         if carry.dtype != x.dtype:
             carry = carry.to(x.dtype)
-    rc = lib.pom_agg_fwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
-                         mask32.stride(0) if mask32 is not None else 0,
-                         mask32.stride(1) if mask32 is not None else 0,
-                         frame_len, ptr(carry), n_past, rope_ptr(rope), out.data_ptr(), ptr(count),
-                         ws.data_ptr(), ws.numel(), stream_handle(x.device))
+    with _Span("agg_fwd"):
+        rc = lib.pom_agg_fwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+                             mask32.stride(0) if mask32 is not None else 0,
+                             mask32.stride(1) if mask32 is not None else 0,
+                             frame_len, ptr(carry), n_past, rope_ptr(rope), out.data_ptr(), ptr(count),
+                             ws.data_ptr(), ws.numel(), stream_handle(x.device))
     check(rc, "pom_agg_fwd")
     return out, count
 
@@ -86,11 +113,12 @@ def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     ws = workspace(x.device, nbytes)
     xv, gv = view3(x), view3(grad_x)
     go32 = go32.contiguous()
-    rc = lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
-                         mask32.stride(0) if mask32 is not None else 0,
-                         mask32.stride(1) if mask32 is not None else 0, ptr(count),
-                         frame_len, n_past, rope_ptr(rope), go32.data_ptr(), ctypes.byref(gv),
-                         gc.data_ptr(), ws.data_ptr(), ws.numel(), stream_handle(x.device))
+    with _Span("agg_bwd"):
+        rc = lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+                             mask32.stride(0) if mask32 is not None else 0,
+                             mask32.stride(1) if mask32 is not None else 0, ptr(count),
+                             frame_len, n_past, rope_ptr(rope), go32.data_ptr(), ctypes.byref(gv),
+                             gc.data_ptr(), ws.data_ptr(), ws.numel(), stream_handle(x.device))
     check(rc, "pom_agg_bwd")
     return gc
 
@@ -103,8 +131,9 @@ def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg32: torch
     G = hagg32.shape[1]
     sh = torch.empty(B, N, P, dtype=ys.dtype, device=ys.device) if out is None else out
     yv, sv = view3(ys), view3(sh)
-    rc = lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G,
-                          rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
+    with _Span("gate_fwd"):
+        rc = lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G,
+                              rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
     check(rc, "pom_gate_fwd")
     return sh
 
@@ -123,9 +152,10 @@ def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg32: torc
     nbytes = lib.pom_gate_workspace_size(dt, B, N, P, G, rk) or _lib.COUNTER_BYTES
     ws = workspace(ys.device, nbytes)
     yv, gv, dv = view3(ys), view3(grad_sh), view3(grad_ys)
-    rc = lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G, rope_ptr(rope),
-                          ctypes.byref(gv), ctypes.byref(dv), gh.data_ptr(), ptr(gb), ws.data_ptr(),
-                          ws.numel(), stream_handle(ys.device))
+    with _Span("gate_bwd"):
+        rc = lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G,
+                              rope_ptr(rope), ctypes.byref(gv), ctypes.byref(dv), gh.data_ptr(), ptr(gb),
+                              ws.data_ptr(), ws.numel(), stream_handle(ys.device))
     check(rc, "pom_gate_bwd")
     return gh, gb
 
@@ -285,7 +315,8 @@ class _PoMLayer(torch.autograd.Function):
         dt = x.dtype
         x2 = x.reshape(B * N, D)
         wq = w_qc if w_qc.dtype == dt else w_qc.to(dt)
-        y = torch.mm(x2, wq.t())                                    # (T, 2P)
+        with _Span("gemm_qc_fwd"):
+            y = torch.mm(x2, wq.t())                                # (T, 2P)
         y3 = y.view(B, N, 2 * P)
         h_view, s_view = y3[..., :P], y3[..., P:]
         c32 = _coeff32(coeff, P, k)
@@ -294,7 +325,8 @@ class _PoMLayer(torch.autograd.Function):
         b32 = se_bias.detach().float().contiguous()
         sh = gate_forward(s_view, b32, h32, rope_s)                 # (B, N, P)
         wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
-        out = torch.mm(sh.view(B * N, P), wa.t())
+        with _Span("gemm_ag_fwd"):
+            out = torch.mm(sh.view(B * N, P), wa.t())
         if b_ag is not None:
             out = out + b_ag.to(dt)
         ctx.save_for_backward(x, y, sh, h32, c32, b32, wq, wa, mask, count)
@@ -314,8 +346,10 @@ class _PoMLayer(torch.autograd.Function):
         g2 = grad_out.reshape(T, D)
         if g2.dtype != dt:
             g2 = g2.to(dt)
-        dsh = torch.mm(g2, wa)                                      # (T, P)
-        dw_ag = torch.mm(g2.t(), sh.view(T, P))                     # (D, P)
+        with _Span("gemm_ag_dgrad"):
+            dsh = torch.mm(g2, wa)                                  # (T, P)
+        with _Span("gemm_ag_wgrad"):
+            dw_ag = torch.mm(g2.t(), sh.view(T, P))                 # (D, P)
         db_ag = g2.float().sum(0) if has_bias else None
         y3 = y.view(B, N, 2 * P)
         dy = torch.empty(T, 2 * P, dtype=dt, device=x.device)
@@ -324,8 +358,10 @@ class _PoMLayer(torch.autograd.Function):
         if grad_hagg is not None:
             dh = dh + grad_hagg.float()
         dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h)
-        dx = torch.mm(dy, wq)                                       # (T, D)
-        dw_qc = torch.mm(dy.t(), x.reshape(T, D))                   # (2P, D)
+        with _Span("gemm_qc_dgrad"):
+            dx = torch.mm(dy, wq)                                   # (T, D)
+        with _Span("gemm_qc_wgrad"):
+            dw_qc = torch.mm(dy.t(), x.reshape(T, D))               # (2P, D)
         g_carry = None
         if has_carry:
             nf = dh.shape[1]
