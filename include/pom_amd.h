@@ -11,17 +11,17 @@
  * last failure on the calling thread.  Invalid arguments are rejected before
  * anything is launched.
  *
- * Workspace: entry points that reduce across workgroups take a workspace of
- * at least the size the matching *_workspace_size() reports.  Its first
- * POM_COUNTER_BYTES bytes hold arrival counters which must be zero before the
- * first use; every call that returns POM_OK leaves them zero again, so one
- * zero-initialised workspace can be reused by any sequence of calls on one
- * stream.  Calls that overlap in time must not share a workspace.
+ * Workspace: entry points that reduce across workgroups take a device
+ * workspace of at least the size the matching *_workspace_size() reports,
+ * 256-byte aligned.  Its contents need no initialisation and are scratch
+ * between calls; calls that may run at the same time (different streams)
+ * must not share one.  The size depends only on the shape arguments of the
+ * size query, so one buffer sized for the largest shape serves every call.
  *
  * Layouts (element strides; the last axis is always contiguous):
  *   x, grad_x, y_s, sh ...  (B, N, C) views  -> pom_view {data, stride_b, stride_n}
  *   coeff, grad_coeff       (P, K) fp32 row-major
- *   aggregate outputs       (B, G, P) contiguous, G = N / frame_len
+ *   aggregate outputs       (B, G, P) contiguous in the element type, G = N / frame_len
  *   mask, count             (B, N) fp32 weights (1 = keep), (B,) fp32
  */
 #ifndef POM_AMD_H
@@ -34,8 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 1
-#define POM_COUNTER_BYTES (1u << 20)
+#define POM_AMD_ABI_VERSION 2
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -85,12 +84,17 @@ const char* pom_last_error(void);
  *   masked mean  mask != NULL (frame_len == N): sum m*p / sum m, an all-zero
  *                row gives 0; tokens with m == 0 are never read
  *                replaces poly_agg_masked_triton          (pom/pom_triton_masked.py:402-428)
- *   frame-causal frame_len < N: output row f = running mean of the frame
- *                means of frames 0..f, carried in the element type after
- *                each frame — the recurrence of PoM.state_forward
- *                (pom/pom.py:233-262) applied to N/frame_len frames at once,
- *                equal to full_mask_mixer with a block-causal 3-D mask
- *                (pom/pom.py:41-45) up to that rounding
+ *   frame-causal 1 < frame_len < N: output row f = running mean of the
+ *                frame means of frames 0..f, evaluated with the element-type
+ *                rounding of every step of PoM.state_forward
+ *                (pom/pom.py:252-259), so it equals a state_forward loop
+ *                over the frames bit for bit, and full_mask_mixer with a
+ *                block-causal 3-D mask (pom/pom.py:41-45) up to that rounding
+ *   token-causal frame_len == 1 (N > 1): output row n = mean of tokens 0..n
+ *                (chunked scan) — replaces poly_agg_causal_triton
+ *                (pom/pom_triton_causal.py:400-423) and, with 1-D RoPE,
+ *                poly_agg_rope_causal_triton (pom/pom_triton_rope.py:1020-1053);
+ *                grad_out must then be contiguous (B, N, P)
  *   state carry  carry != NULL: (B, P) previous 'h' in the element type and
  *                n_past previous calls; frame 0 continues that recurrence
  *   RoPE         rope->kind 1-D / 2-D: each token's p is rotated before it is
@@ -101,8 +105,8 @@ const char* pom_last_error(void);
 size_t pom_agg_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int K,
                               int64_t frame_len, int rope_kind, int backward);
 
-/* Forward.  out: (B, N/frame_len, P) in dtype.  count_out: (B,) fp32 sum of
- * mask weights (masked mode; may be NULL). */
+/* Forward.  out: (B, N/frame_len, P) contiguous in dtype.  count_out: (B,)
+ * fp32 sum of the mask weights (masked mode; required there). */
 int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
                 const pom_view* x, const float* coeff,
                 const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
@@ -128,19 +132,20 @@ int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
 /* ------------------------------------------------------------------------
  * Gating (pom/pom.py:207, :103-122; query-side RoPE pom/pom_rope.py:522):
  *   sh = R(pos) hardsigmoid(y_s + bias) * hagg[b, n / (N / groups)]
- * hagg: (B, groups, P) fp32.  bias: (P,) fp32 or NULL.
+ * hagg: (B, groups, P) contiguous in the element type (the aggregation's
+ * output; groups == N gives one row per token).  bias: (P,) fp32 or NULL.
  * ------------------------------------------------------------------------ */
 size_t pom_gate_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t groups,
                                int rope_kind);
 
 int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P,
-                 const pom_view* ys, const float* bias, const float* hagg, int64_t groups,
+                 const pom_view* ys, const float* bias, const void* hagg, int64_t groups,
                  const pom_rope* rope, const pom_view* sh, void* stream);
 
 /* Backward.  grad_ys: view (e.g. the s-half of dY) receiving dL/dy_s.
- * grad_hagg: (B, groups, P) fp32.  grad_bias: (P,) fp32 or NULL. */
+ * grad_hagg: (B, groups, P) fp32, 16-byte aligned.  grad_bias: (P,) fp32 or NULL. */
 int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P,
-                 const pom_view* ys, const float* bias, const float* hagg, int64_t groups,
+                 const pom_view* ys, const float* bias, const void* hagg, int64_t groups,
                  const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
                  float* grad_hagg, float* grad_bias,
                  void* workspace, size_t workspace_bytes, void* stream);

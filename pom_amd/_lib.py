@@ -25,8 +25,8 @@ POM_ERR_DEVICE = 4
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
-COUNTER_BYTES = 1 << 20
 MAX_DEGREE = 16
+ABI_VERSION = 2
 
 # Every symbol include/pom_amd.h declares, with its ctypes signature.
 _c_i64 = ctypes.c_int64
@@ -83,7 +83,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.pom_abi_version() != 1:
+        if lib.pom_abi_version() != ABI_VERSION:
             raise RuntimeError("pom_amd: ABI version mismatch; rebuild libpom_amd.so")
         _lib = lib
     return _lib
@@ -145,20 +145,18 @@ _ws_lock = threading.Lock()
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised workspace for one (device, stream).
+    """Scratch workspace for one (device, stream); contents need no initialisation.
 
-    The library leaves the counter prefix zero after every successful call, so
-    the buffer is reused across calls on the same stream; a larger request
-    allocates a new zeroed buffer (stream-ordered, so the old one may still be
-    in use by queued kernels until the allocator recycles it).
+    Calls on one stream run in order, so they share the buffer; a larger
+    request replaces it with a bigger one (the caching allocator keeps the old
+    block alive until the queued kernels that use it have run).
     """
     stream = torch.cuda.current_stream(device)
     key = (device.index, stream.cuda_stream)
     with _ws_lock:
         buf = _ws_cache.get(key)
         if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, COUNTER_BYTES + (4 << 20))
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             _ws_cache[key] = buf
         return buf
 

@@ -1,0 +1,606 @@
+// Fused activation + polynomial expansion + sequence aggregation (forward and
+// backward) for the Polynomial Mixer, written for gfx950 (CDNA4).
+//
+// One kernel family covers the reference's mean, masked, frame-causal and RoPE
+// aggregations (pom/pom_triton.py:68-321, pom/pom_triton_masked.py:72-345,
+// pom/pom.py:233-262 + :41-45, pom/pom_triton_rope.py:93-475,
+// pom/pom_rope.py:242-296).
+//
+// Work decomposition:
+//   grid = (slabs, chunks, B), 256 threads (4 waves) per workgroup.
+//   A workgroup streams the rows of one chunk of one batch row through one
+//   channel slab.  Within a wave, 2^lpr_log2 lanes cover one token row (each
+//   lane cpt consecutive units, one 16-byte load for bf16) and 64/2^lpr_log2
+//   rows are processed side by side; the four waves interleave rows.  Loads of
+//   U rows are issued before any arithmetic so every lane keeps U 16-byte
+//   loads in flight.  Accumulation is fp32 in registers.
+//   At the end, lanes sharing a column are summed with cross-lane shuffles,
+//   the four waves through LDS, and the chunk's result is written either as
+//   the final output (one chunk per batch row) or as an fp32 partial that a
+//   finalize kernel sums in a fixed order.  No floating-point atomics and no
+//   inter-workgroup synchronisation: results are deterministic run to run.
+//
+// Frames: tokens are grouped in F frames of L tokens (F = 1 for the plain
+// mean).  The finalize kernel turns frame sums into frame means and runs the
+// running-mean recurrence of PoM.state_forward across frames
+// (pom/pom.py:255-259) with the reference's rounding in the element type, so
+// a full-sequence frame-causal call and the frame-by-frame state_forward loop
+// produce identical bits.
+#pragma once
+
+#include "common.h"
+#include "pom_internal.h"
+#include "lanes.h"
+
+namespace pom {
+
+struct LaneGeom {
+  int tid, wave, lane, lb, lpr, rpw, rs, lrow, lcol;
+  __device__ __forceinline__ explicit LaneGeom(int lpr_log2) {
+    tid = threadIdx.x;
+    wave = tid / kWave;
+    lane = tid % kWave;
+    lb = lpr_log2;
+    lpr = 1 << lb;
+    rpw = kWave >> lb;          // rows per wave step
+    rs = kWaves * rpw;          // rows per workgroup step
+    lrow = lane >> lb;
+    lcol = lane & (lpr - 1);
+  }
+};
+
+// Row range of chunk `chunk` (frames never straddled).
+__device__ __forceinline__ void chunk_rows(const Geom& g, int64_t chunk, int64_t N, int64_t& f, int64_t& rbeg,
+                                           int64_t& rend) {
+  f = chunk / g.cpf;
+  rbeg = f * g.L + (chunk - f * g.cpf) * g.RC;
+  const int64_t fe = (f + 1) * g.L;
+  rend = rbeg + g.RC < fe ? rbeg + g.RC : fe;
+  if (rend > N) rend = N;
+}
+
+template <int MODE>
+struct Mode_ {
+  static constexpr bool rope = (MODE == MODE_ROPE1D || MODE == MODE_ROPE2D);
+  static constexpr int U = rope ? 4 : 8;   // rows in flight per lane
+};
+
+// Rows of a chunk as seen by one lane: step `it` covers rows
+// base + row0 + u * rs (u < U), base = it * rs * U.  Every step but the last
+// is full; the last clamps its row indices into the chunk (so every load
+// stays in bounds and is issued without a branch) and its compute drops the
+// rows past the end.
+struct RowWalk {
+  int64_t rbeg, nrows, step;
+  int row0, rs;
+  __device__ __forceinline__ RowWalk(int64_t rbeg_, int64_t rend_, int row0_, int rs_, int U)
+      : rbeg(rbeg_), nrows(rend_ - rbeg_), step((int64_t)rs_ * U), row0(row0_), rs(rs_) {}
+  __device__ __forceinline__ int64_t full_steps() const { return nrows / step; }
+  __device__ __forceinline__ bool has_tail() const { return full_steps() * step < nrows; }
+  __device__ __forceinline__ bool valid(int64_t base, int u) const { return base + row0 + (int64_t)u * rs < nrows; }
+  // absolute row; clamped into the chunk when `clamp`
+  __device__ __forceinline__ int64_t row(int64_t base, int u, bool clamp) const {
+    int64_t rel = base + row0 + (int64_t)u * rs;
+    if (clamp && rel >= nrows) rel = nrows - 1;
+    return rbeg + rel;
+  }
+};
+
+// Masked mode: the chunk's first and last rows with a nonzero weight and the
+// sum of its weights, from one pass over the chunk's mask entries.  Rows
+// outside [first, last] are never loaded.
+__device__ __forceinline__ void mask_extent(const AggParams& p, int64_t b, int64_t rbeg, int64_t rend,
+                                            int64_t& first, int64_t& last, float& total) {
+  __shared__ int64_t s_first[kWaves], s_last[kWaves];
+  __shared__ float s_tot[kWaves];
+  int64_t lo = rend, hi = rbeg - 1;
+  float t = 0.0f;
+  for (int64_t n = rbeg + threadIdx.x; n < rend; n += kThreads) {
+    const float m = p.mask[b * p.msb + n * p.msn];
+    if (m != 0.0f) {
+      lo = n < lo ? n : lo;
+      hi = n > hi ? n : hi;
+      t += m;
+    }
+  }
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t olo = __shfl_xor(lo, off, kWave), ohi = __shfl_xor(hi, off, kWave);
+    lo = olo < lo ? olo : lo;
+    hi = ohi > hi ? ohi : hi;
+    t += __shfl_xor(t, off, kWave);
+  }
+  const int wave = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) {
+    s_first[wave] = lo;
+    s_last[wave] = hi;
+    s_tot[wave] = t;
+  }
+  __syncthreads();
+  first = s_first[0];
+  last = s_last[0];
+  total = s_tot[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    first = s_first[w] < first ? s_first[w] : first;
+    last = s_last[w] > last ? s_last[w] : last;
+    total += s_tot[w];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward chunk kernel
+// ---------------------------------------------------------------------------
+template <typename T, int CPT, int KM, int MODE>
+__global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
+  using Map = LaneMap<CPT, MODE>;
+  constexpr int CPT2 = Map::CPT2;
+  constexpr bool ROPE = Mode_<MODE>::rope;
+  constexpr bool MASKED = MODE == MODE_MASKED;
+  constexpr int U = Mode_<MODE>::U;
+  __shared__ float red[kWaves][16 * CPT2];
+
+  const LaneGeom G(p.g.lpr_log2);
+  const int64_t slab = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
+  int64_t f, rbeg, rend;
+  chunk_rows(p.g, chunk, p.N, f, rbeg, rend);
+  float total = 0.0f;
+  if constexpr (MASKED) {
+    int64_t first, last;
+    mask_extent(p, b, rbeg, rend, first, last, total);
+    rbeg = first;
+    rend = last >= first ? last + 1 : first;   // empty when the chunk has no valid row
+  }
+  const int64_t vcol = slab * G.lpr + G.lcol;
+  const bool active = vcol < p.g.nvec;
+  Map map;
+  map.init(active ? vcol : 0, p.P);
+
+  float c[CPT2][KM];
+#pragma unroll
+  for (int i = 0; i < CPT2; ++i)
+#pragma unroll
+    for (int j = 0; j < KM; ++j) c[i][j] = (active && j < p.K) ? p.coeff[map.chan(i) * p.K + j] : 0.0f;
+
+  float acc[CPT2];
+#pragma unroll
+  for (int i = 0; i < CPT2; ++i) acc[i] = 0.0f;
+
+  const T* xb = reinterpret_cast<const T*>(p.x) + b * p.sxb;
+  const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+
+  auto step = [&](int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    Pack<T, CPT> v1[U], v2[ROPE ? U : 1];
+    float wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t rr = W.row(base, u, TAIL);
+      const T* row = xb + rr * p.sxn;
+      v1[u].load(row + map.c1);
+      if constexpr (ROPE) v2[u].load(row + map.c2);
+      if constexpr (MASKED) wv[u] = p.mask[b * p.msb + rr * p.msn];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bool keep = !TAIL || W.valid(base, u);
+      if constexpr (MASKED) keep = keep && wv[u] != 0.0f;   // also drops NaN padding
+      if constexpr (ROPE) {
+        float cs[CPT], sn[CPT];
+        load_table<CPT>(p.rope, map.table, W.row(base, u, TAIL), map.tcol, cs, sn);
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          float h1 = act(v1[u].get(i)), h2 = act(v2[u].get(i));
+          if (TAIL) {
+            h1 = keep ? h1 : 0.0f;
+            h2 = keep ? h2 : 0.0f;
+          }
+          const float p1 = poly<KM>(h1, c[i]);
+          const float p2 = poly<KM>(h2, c[CPT + i]);
+          acc[i] += p1 * cs[i] - p2 * sn[i];
+          acc[CPT + i] += p2 * cs[i] + p1 * sn[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          float h = act(v1[u].get(i));
+          if (TAIL || MASKED) h = keep ? h : 0.0f;   // p(0) = 0
+          const float q = poly_q<KM>(h, c[i]);
+          if constexpr (MASKED) acc[i] = fmaf(q, h * wv[u], acc[i]);
+          else acc[i] = fmaf(q, h, acc[i]);
+        }
+      }
+    }
+  };
+
+  if (active) {
+    const int64_t nfull = W.full_steps();
+    for (int64_t it = 0; it < nfull; ++it) step(it * W.step, std::false_type{});
+    if (W.has_tail()) step(nfull * W.step, std::true_type{});
+  }
+
+  // Rows -> one value per column: shuffles inside the wave, LDS across waves.
+#pragma unroll
+  for (int i = 0; i < CPT2; ++i) acc[i] = xor_sum_rows(acc[i], G.lb);
+  if (G.lrow == 0) {
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) red[G.wave][G.lcol * CPT2 + i] = acc[i];
+  }
+  __syncthreads();
+  const int nslot = G.lpr * CPT2;
+  for (int s = G.tid; s < nslot; s += kThreads) {
+    const int l = s / CPT2, i = s - l * CPT2;
+    const int64_t vc = slab * G.lpr + l;
+    if (vc >= p.g.nvec) continue;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += red[w][s];
+    Map m2;
+    m2.init(vc, p.P);
+    const int64_t ch = m2.chan(i);
+    if (p.direct) {
+      float mean;
+      if constexpr (MASKED) mean = total != 0.0f ? v / total : 0.0f;   // empty row -> 0
+      else mean = v / (float)p.g.L;
+      reinterpret_cast<T*>(p.out)[b * p.P + ch] = from_f32<T>(mean);
+    } else {
+      p.part[(b * p.g.nch + chunk) * p.P + ch] = v;
+    }
+  }
+  if constexpr (MASKED) {
+    if (slab == 0 && G.tid == 0) {
+      if (p.direct) {
+        if (p.count_out) p.count_out[b] = total;
+      } else {
+        p.pcnt[b * p.g.nch + chunk] = total;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward finalize: chunk sums -> frame means -> running-mean recurrence.
+// One thread per (batch row, channel).
+// ---------------------------------------------------------------------------
+template <typename T, bool MASKED>
+__global__ void __launch_bounds__(kThreads) agg_fwd_finalize(const AggParams p) {
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= p.B * p.P) return;
+  const int64_t b = idx / p.P, c = idx - b * p.P;
+  const int64_t nch = p.g.nch, cpf = p.g.cpf, F = p.g.F;
+  const float* part = p.part + b * nch * p.P + c;
+  float cnt = 0.0f;
+  if (MASKED) {
+    for (int64_t k = 0; k < nch; ++k) cnt += p.pcnt[b * nch + k];
+    if (c == 0 && p.count_out) p.count_out[b] = cnt;
+  }
+  T* out = reinterpret_cast<T*>(p.out) + b * F * p.P + c;
+  const bool recur = F > 1 || p.carry != nullptr;
+  bool have = p.carry != nullptr;
+  float h = have ? to_f32<T>(reinterpret_cast<const T*>(p.carry)[b * p.P + c]) : 0.0f;
+  float n = (float)p.n_past;
+  for (int64_t f = 0; f < F; ++f) {
+    float s = 0.0f;
+    for (int64_t k = 0; k < cpf; ++k) s += part[(f * cpf + k) * p.P];
+    const float m = MASKED ? (cnt != 0.0f ? s / cnt : 0.0f) : s / (float)p.g.L;
+    if (!recur) {
+      out[0] = from_f32<T>(m);
+      return;
+    }
+    // The per-frame mean is a tensor of the element type in the reference
+    // (pom/pom_triton.py:348) before it enters the recurrence.
+    const float mt = round_to<T>(m);
+    h = have ? running_mean_step<T>(h, mt, n) : mt;
+    have = true;
+    out[f * p.P] = from_f32<T>(h);
+    n += 1.0f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: per-frame token weights for F > 1 frames.
+//   dM_f = sum_{g >= f} dH_g / (n_past + g + 1),   token weight = dM_f / L
+// ---------------------------------------------------------------------------
+static __global__ void __launch_bounds__(kThreads) agg_frame_weights(const AggParams p, float* wf) {
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= p.B * p.P) return;
+  const int64_t b = idx / p.P, c = idx - b * p.P;
+  const int64_t F = p.g.F;
+  float s = 0.0f;
+  for (int64_t f = F - 1; f >= 0; --f) {
+    s += p.go[(b * F + f) * p.P + c] / ((float)(p.n_past + f) + 1.0f);
+    wf[(b * F + f) * p.P + c] = s / (float)p.g.L;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward chunk kernel: grad_x for every row of the chunk (written into a
+// strided view, e.g. the h-half of dY) and the chunk's grad_coeff partial.
+// ---------------------------------------------------------------------------
+template <typename T, int CPT, int KM, int MODE>
+__global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
+  using Map = LaneMap<CPT, MODE>;
+  constexpr int CPT2 = Map::CPT2;
+  constexpr bool ROPE = Mode_<MODE>::rope;
+  constexpr bool MASKED = MODE == MODE_MASKED;
+  constexpr int U = Mode_<MODE>::U;
+  __shared__ float red[kWaves][16 * CPT2];
+
+  const LaneGeom G(p.g.lpr_log2);
+  const int64_t slab = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
+  int64_t f, rbeg, rend;
+  chunk_rows(p.g, chunk, p.N, f, rbeg, rend);
+  const int64_t vcol = slab * G.lpr + G.lcol;
+  const bool active = vcol < p.g.nvec;
+  Map map;
+  map.init(active ? vcol : 0, p.P);
+
+  // d[i][j] = (j+1) c[i][j]; w = the gradient weight of one token of this frame.
+  float d[CPT2][KM], g[CPT2][KM], w[CPT2];
+  float cntv = 1.0f;
+  if constexpr (MASKED) cntv = p.count_in[b];
+#pragma unroll
+  for (int i = 0; i < CPT2; ++i) {
+    const int64_t ch = map.chan(i);
+#pragma unroll
+    for (int j = 0; j < KM; ++j) {
+      d[i][j] = (active && j < p.K) ? p.coeff[ch * p.K + j] * (float)(j + 1) : 0.0f;
+      g[i][j] = 0.0f;
+    }
+    float wi = 0.0f;
+    if (active) {
+      if constexpr (MASKED) {
+        wi = cntv != 0.0f ? p.go[b * p.P + ch] / cntv : 0.0f;
+      } else if (p.wf) {
+        wi = p.wf[(b * p.g.F + f) * p.P + ch];
+      } else {
+        wi = (p.go[b * p.P + ch] / ((float)p.n_past + 1.0f)) / (float)p.g.L;
+      }
+    }
+    w[i] = wi;
+  }
+  float w01[CPT2];
+#pragma unroll
+  for (int i = 0; i < CPT2; ++i) w01[i] = 0.01f * w[i];
+
+  const T* xb = reinterpret_cast<const T*>(p.x) + b * p.sxb;
+  T* gxb = reinterpret_cast<T*>(p.gx) + b * p.sgb;
+  if constexpr (MASKED) {
+    // Rows before the first and after the last valid row get a zero gradient
+    // without their x being read.
+    int64_t first, last;
+    float unused;
+    mask_extent(p, b, rbeg, rend, first, last, unused);
+    if (last < first) first = last = rend;   // no valid row: zero the whole chunk
+    else ++last;
+    if (active) {
+      float z[CPT];
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) z[i] = 0.0f;
+      for (int64_t n = rbeg + G.wave * G.rpw + G.lrow; n < first; n += G.rs)
+        VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
+      for (int64_t n = last + G.wave * G.rpw + G.lrow; n < rend; n += G.rs)
+        VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
+    }
+    rbeg = first;
+    rend = last;
+  }
+  const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+
+  auto step = [&](int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    Pack<T, CPT> v1[U], v2[ROPE ? U : 1];
+    float mv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t rr = W.row(base, u, TAIL);
+      const T* row = xb + rr * p.sxn;
+      v1[u].load(row + map.c1);
+      if constexpr (ROPE) v2[u].load(row + map.c2);
+      if constexpr (MASKED) mv[u] = p.mask[b * p.msb + rr * p.msn];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool in = !TAIL || W.valid(base, u);
+      const int64_t n = W.row(base, u, TAIL);
+      T* grow = gxb + n * p.sgn;
+      float gv1[CPT], gv2[CPT];
+      if constexpr (ROPE) {
+        float cs[CPT], sn[CPT];
+        load_table<CPT>(p.rope, map.table, n, map.tcol, cs, sn);
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {   // R^T applied to (w1, w2)
+          const float wa = w[i] * cs[i] + w[CPT + i] * sn[i];
+          const float wb = w[CPT + i] * cs[i] - w[i] * sn[i];
+          const float x1 = v1[u].get(i), x2 = v2[u].get(i);
+          const float l1 = leaky(x1), l2 = leaky(x2);
+          const float h1 = clamp_act(l1), h2 = clamp_act(l2);
+          gv1[i] = weighted_act_grad(x1, l1, h1, wa, 0.01f * wa) * poly_d<KM>(h1, d[i]);
+          gv2[i] = weighted_act_grad(x2, l2, h2, wb, 0.01f * wb) * poly_d<KM>(h2, d[CPT + i]);
+          pow_acc<KM>(in ? h1 : 0.0f, wa, g[i]);
+          pow_acc<KM>(in ? h2 : 0.0f, wb, g[CPT + i]);
+        }
+        if (in) {
+          VecIO<T, CPT>::store(grow + map.c1, gv1);
+          VecIO<T, CPT>::store(grow + map.c2, gv2);
+        }
+      } else {
+        bool keep = in;
+        if constexpr (MASKED) keep = keep && mv[u] != 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const float xx = v1[u].get(i);
+          const float l = leaky(xx), h = clamp_act(l);
+          if constexpr (MASKED) {
+            const float wt = w[i] * mv[u];
+            const float gxv = weighted_act_grad(xx, l, h, wt, 0.01f * wt) * poly_d<KM>(h, d[i]);
+            gv1[i] = keep ? gxv : 0.0f;   // padded token: zero gradient
+            pow_acc<KM>(keep ? h : 0.0f, wt, g[i]);
+          } else {
+            gv1[i] = weighted_act_grad(xx, l, h, w[i], w01[i]) * poly_d<KM>(h, d[i]);
+            pow_sum<KM>(TAIL ? (in ? h : 0.0f) : h, g[i]);   // scaled by w at the end
+          }
+        }
+        if (in) VecIO<T, CPT>::store(grow + map.c1, gv1);
+      }
+    }
+  };
+
+  if (active) {
+    const int64_t nfull = W.full_steps();
+    for (int64_t it = 0; it < nfull; ++it) step(it * W.step, std::false_type{});
+    if (W.has_tail()) step(nfull * W.step, std::true_type{});
+  }
+  if constexpr (!ROPE && !MASKED) {
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i)
+#pragma unroll
+      for (int j = 0; j < KM; ++j) g[i][j] *= w[i];
+  }
+
+  // grad_coeff partial of the chunk, one degree at a time.
+  const int nslot = G.lpr * CPT2;
+  for (int j = 0; j < p.K; ++j) {
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) {
+      float v = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < KM; ++jj) v = (jj == j) ? g[i][jj] : v;
+      v = xor_sum_rows(v, G.lb);
+      if (G.lrow == 0) red[G.wave][G.lcol * CPT2 + i] = v;
+    }
+    __syncthreads();
+    for (int s = G.tid; s < nslot; s += kThreads) {
+      const int l = s / CPT2, i = s - l * CPT2;
+      const int64_t vc = slab * G.lpr + l;
+      if (vc >= p.g.nvec) continue;
+      float v = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < kWaves; ++w2) v += red[w2][s];
+      Map m2;
+      m2.init(vc, p.P);
+      p.part[((b * p.g.nch + chunk) * p.K + j) * p.P + m2.chan(i)] = v;
+    }
+    __syncthreads();
+  }
+}
+
+// grad_coeff[c, j] = sum over (batch row, chunk) of the partials, fixed order.
+static __global__ void __launch_bounds__(kThreads) coeff_grad_finalize(const float* __restrict__ part, int64_t rows,
+                                                                int64_t P, int K, float* __restrict__ gc) {
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (idx >= P * K) return;
+  const int64_t j = idx / P, c = idx - j * P;
+  const float* src = part + j * P + c;
+  const int64_t stride = (int64_t)K * P;
+  float s = 0.0f;
+  int64_t r = 0;
+  for (; r + 8 <= rows; r += 8) {   // eight loads in flight, summed in row order
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = src[(r + q) * stride];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += v[q];
+  }
+  for (; r < rows; ++r) s += src[r * stride];
+  gc[c * K + j] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch helpers
+// ---------------------------------------------------------------------------
+inline dim3 flat_grid(int64_t n) { return dim3((unsigned)((n + kThreads - 1) / kThreads)); }
+
+template <typename T, int CPT, int KM>
+hipError_t agg_fwd_mode(const AggParams& p, hipStream_t st) {
+  const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
+  switch (p.mode) {
+    case MODE_PLAIN: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_PLAIN>), grid, block, 0, st, p); break;
+    case MODE_MASKED: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_MASKED>), grid, block, 0, st, p); break;
+    case MODE_ROPE1D: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_ROPE1D>), grid, block, 0, st, p); break;
+    case MODE_ROPE2D: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_ROPE2D>), grid, block, 0, st, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename T, int CPT, int KM>
+hipError_t agg_bwd_mode(const AggParams& p, hipStream_t st) {
+  const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
+  switch (p.mode) {
+    case MODE_PLAIN: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_PLAIN>), grid, block, 0, st, p); break;
+    case MODE_MASKED: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_MASKED>), grid, block, 0, st, p); break;
+    case MODE_ROPE1D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D>), grid, block, 0, st, p); break;
+    case MODE_ROPE2D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D>), grid, block, 0, st, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Degree bound KM: exact for K <= 4, then 8 and 16 with zero coefficients.
+#define POM_K_SWITCH(K_, CALL)                   \
+  switch (K_) {                                  \
+    case 1: { constexpr int KM = 1; CALL; }      \
+    case 2: { constexpr int KM = 2; CALL; }      \
+    case 3: { constexpr int KM = 3; CALL; }      \
+    case 4: { constexpr int KM = 4; CALL; }      \
+    default: break;                              \
+  }                                              \
+  if ((K_) <= 8) { constexpr int KM = 8; CALL; } \
+  { constexpr int KM = 16; CALL; }
+
+template <typename T, int CPT>
+hipError_t agg_fwd_cpt(const AggParams& p, hipStream_t st) {
+  POM_K_SWITCH(p.K, return (agg_fwd_mode<T, CPT, KM>(p, st)))
+}
+
+template <typename T, int CPT>
+hipError_t agg_bwd_cpt(const AggParams& p, hipStream_t st) {
+  POM_K_SWITCH(p.K, return (agg_bwd_mode<T, CPT, KM>(p, st)))
+}
+
+// Vector widths: 16-byte loads when pointers and strides allow, else narrower.
+#define POM_CPT_SWITCH(T_, CPT_, FN, ...)                                   \
+  switch (CPT_) {                                                           \
+    case 8: if constexpr (sizeof(T_) == 2) return FN<T_, 8>(__VA_ARGS__); else break; \
+    case 4: return FN<T_, 4>(__VA_ARGS__);                                  \
+    case 2: return FN<T_, 2>(__VA_ARGS__);                                  \
+    case 1: return FN<T_, 1>(__VA_ARGS__);                                  \
+    default: break;                                                         \
+  }                                                                         \
+  return hipErrorInvalidValue;
+
+template <typename T>
+hipError_t agg_fwd_chunks(const AggParams& p, hipStream_t st) {
+  POM_CPT_SWITCH(T, p.g.cpt, agg_fwd_cpt, p, st)
+}
+
+template <typename T>
+hipError_t agg_bwd_chunks(const AggParams& p, hipStream_t st) {
+  POM_CPT_SWITCH(T, p.g.cpt, agg_bwd_cpt, p, st)
+}
+
+template <typename T>
+hipError_t agg_fwd_t(const AggParams& p, hipStream_t st) {
+  hipError_t e = agg_fwd_chunks<T>(p, st);
+  if (e != hipSuccess || p.direct) return e;
+  if (p.mode == MODE_MASKED)
+    hipLaunchKernelGGL((agg_fwd_finalize<T, true>), flat_grid(p.B * p.P), dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((agg_fwd_finalize<T, false>), flat_grid(p.B * p.P), dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t agg_bwd_t(const AggParams& p, hipStream_t st) {
+  if (p.wf) {
+    hipLaunchKernelGGL(agg_frame_weights, flat_grid(p.B * p.P), dim3(kThreads), 0, st, p,
+                       const_cast<float*>(p.wf));
+    if (hipError_t e = hipGetLastError()) return e;
+  }
+  if (hipError_t e = agg_bwd_chunks<T>(p, st)) return e;
+  hipLaunchKernelGGL(coeff_grad_finalize, flat_grid(p.P * p.K), dim3(kThreads), 0, st, p.part,
+                     p.B * p.g.nch, p.P, p.K, p.gc);
+  return hipGetLastError();
+}
+
+}  // namespace pom

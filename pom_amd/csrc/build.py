@@ -15,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ["agg.hip", "gate.hip", "capi.cpp"]
+SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "capi.cpp"]
 OUT = os.path.join(PKG, "libpom_amd.so")
 BUILD_DIR = os.path.join(PKG, "_build")
 
@@ -30,8 +30,19 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
+def _stale(src: str, obj: str) -> bool:
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    deps = [os.path.join(HERE, f) for f in os.listdir(HERE) if f.endswith((".h", ".hip", ".cpp"))]
+    deps.append(os.path.join(ROOT, "include", "pom_amd.h"))
+    return any(os.path.getmtime(d) > t for d in deps if d.endswith(".h") or d == os.path.join(HERE, src))
+
+
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    if incremental and not _stale(src, obj):
+        return obj
     lang = ["-x", "hip"]
     cmd = [HIPCC, *FLAGS, *lang, "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -41,10 +52,11 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int = 4, verbose: bool = True) -> str:
+def build(jobs: int = 4, verbose: bool = True, incremental: bool = False) -> str:
+    """Compile every source (or, with incremental=True, only stale objects) and link."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda s: _compile(s, incremental), SOURCES))
     tmp = OUT + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -60,5 +72,6 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
+    ap.add_argument("--incremental", action="store_true", help="recompile only stale objects")
     a = ap.parse_args()
-    build(a.jobs)
+    build(a.jobs, incremental=a.incremental)

@@ -9,6 +9,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace pom {
 
 constexpr int kWave = 64;          // CDNA wavefront width
@@ -92,42 +94,91 @@ __device__ __forceinline__ void store_f32(float* __restrict__ p, const float (&v
 //   act'(x) = (x > 0 ? 1 : 0.01) * [-0.1 <= leaky(x) <= 6]
 // leaky_relu's backward uses x > 0, clamp's backward keeps both bounds.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float leaky(float x) { return x > 0.0f ? x : x * 0.01f; }
+// leaky_relu(x, 0.01) == max(x, 0.01 x) for every x (slope below 1).
+__device__ __forceinline__ float leaky(float x) { return fmaxf(x, 0.01f * x); }
 
-__device__ __forceinline__ float act(float x) {
-  return fminf(fmaxf(leaky(x), -0.1f), 6.0f);
-}
+// clamp(l, -0.1, 6) as one median-of-three.
+__device__ __forceinline__ float clamp_act(float l) { return __builtin_amdgcn_fmed3f(l, -0.1f, 6.0f); }
+
+__device__ __forceinline__ float act(float x) { return clamp_act(leaky(x)); }
 
 __device__ __forceinline__ float act_grad(float x) {
   const float l = leaky(x);
   const float slope = x > 0.0f ? 1.0f : 0.01f;
-  return (l >= -0.1f && l <= 6.0f) ? slope : 0.0f;
+  return (clamp_act(l) == l) ? slope : 0.0f;
 }
 
-// p(h) = sum_{j<K} c[j] h^(j+1), with powers built by repeated products.
+// w * act'(x) given l = leaky(x), h = clamp_act(l), w1 = w and w01 = 0.01 w:
+// leaky_relu's backward picks the slope by x > 0 and clamp's backward passes
+// the gradient where l lies inside [-0.1, 6] (h == l).
+__device__ __forceinline__ float weighted_act_grad(float x, float l, float h, float w1, float w01) {
+  const float s = x > 0.0f ? w1 : w01;
+  return h == l ? s : 0.0f;
+}
+
+// p(h) / h = c0 + h (c1 + h (c2 + ...)) in Horner form, so p(h) = h * poly_q(h).
+template <int K>
+__device__ __forceinline__ float poly_q(float h, const float (&c)[K]) {
+  float t = c[K - 1];
+#pragma unroll
+  for (int j = K - 2; j >= 0; --j) t = fmaf(t, h, c[j]);
+  return t;
+}
+
+// p(h) = sum_{j<K} c[j] h^(j+1).
 template <int K>
 __device__ __forceinline__ float poly(float h, const float (&c)[K]) {
-  float hp = h, acc = c[0] * h;
+  return poly_q<K>(h, c) * h;
+}
+
+// p'(h) = sum_j d[j] h^j with d[j] = (j+1) c[j] precomputed.
+template <int K>
+__device__ __forceinline__ float poly_d(float h, const float (&d)[K]) {
+  return poly_q<K>(h, d);
+}
+
+// g[j] += w h^(j+1) for j < K (the last term as one fma).
+template <int K>
+__device__ __forceinline__ void pow_acc(float h, float w, float (&g)[K]) {
+  float t = w;   // w h^j
 #pragma unroll
-  for (int j = 1; j < K; ++j) {
-    hp *= h;
-    acc += c[j] * hp;
+  for (int j = 0; j < K; ++j) {
+    if (j + 1 == K) {
+      g[j] = fmaf(t, h, g[j]);
+    } else {
+      t *= h;
+      g[j] += t;
+    }
   }
-  return acc;
+}
+
+// g[j] += h^(j+1) for j < K (unweighted power sums).
+template <int K>
+__device__ __forceinline__ void pow_sum(float h, float (&g)[K]) {
+  float t = h;   // h^(j+1)
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    if (j + 1 == K) {
+      g[j] += t;
+    } else if (j + 2 == K) {
+      g[j] += t;
+      g[j + 1] = fmaf(t, h, g[j + 1]);
+      break;
+    } else {
+      g[j] += t;
+      t *= h;
+    }
+  }
 }
 
 // Backward of p at h: returns p'(h) and accumulates w * h^(j+1) into g[j].
 template <int K>
 __device__ __forceinline__ float poly_grad_acc(float h, float w, const float (&c)[K], float (&g)[K]) {
-  float hp = 1.0f, dp = 0.0f;
+  float d[K];
 #pragma unroll
-  for (int j = 0; j < K; ++j) {
-    const float hph = hp * h;
-    dp += c[j] * (float)(j + 1) * hp;
-    g[j] += w * hph;
-    hp = hph;
-  }
-  return dp;
+  for (int j = 0; j < K; ++j) d[j] = c[j] * (float)(j + 1);
+  pow_acc<K>(h, w, g);
+  return poly_d<K>(h, d);
 }
 
 // Hardsigmoid relu6(z + 3) / 6 and its derivative (torch: 1/6 on (-3, 3)).
@@ -139,26 +190,46 @@ __device__ __forceinline__ float hsig_grad(float z) {
 }
 
 // ---------------------------------------------------------------------------
-// Device-scope "last workgroup done" election.
-//
-// Every workgroup of a group publishes its partial results, then calls
-// elect_last(); exactly one workgroup (the last to arrive) gets true and may
-// read all partials of the group.  The counter is reset by the winner so the
-// workspace is reusable by the next launch on the stream without a memset.
+// Raw vector of V elements of T held in registers as loaded (16-byte or
+// narrower memory operations), widened to fp32 one element at a time.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool elect_last(int* counter, int expected, int* lds_flag) {
-  __threadfence();   // every thread releases its own partial stores at agent scope
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = (prev == expected - 1);
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *lds_flag = last ? 1 : 0;
+template <typename T, int V>
+struct Pack {
+  using IO = VecIO<T, V>;
+  typename IO::Raw r[IO::kOps];
+
+  __device__ __forceinline__ void load(const T* __restrict__ p) {
+#pragma unroll
+    for (int op = 0; op < IO::kOps; ++op) r[op] = *reinterpret_cast<const typename IO::Raw*>(p + op * IO::kPer);
   }
-  __syncthreads();
-  const bool last = *lds_flag != 0;
-  if (last) __threadfence();  // acquire: partials of the other workgroups are visible
-  return last;
+  __device__ __forceinline__ float get(int i) const {
+    return to_f32<T>(reinterpret_cast<const T*>(r)[i]);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Cross-lane sums inside one 64-lane wavefront: lanes whose ids differ only in
+// bits >= lo_bits (the lanes that share a column) are added, fixed order.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float xor_sum_rows(float v, int lo_bits) {
+  for (int off = 1 << lo_bits; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// The running-mean step of PoM.state_forward (pom/pom.py:255-259) as the
+// reference evaluates it on the GPU in the element type T:
+//   a = T(n * h)              (scalar multiply in fp32, rounded)
+//   c = T(a + m)              (the n_current = 1 term is m itself)
+//   h = T(c * fp32(1/(n+1)))  (division by a scalar is a multiply by its
+//                              fp32 reciprocal in torch's GPU kernels)
+// The _rn intrinsics keep the compiler from contracting into an fma.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float running_mean_step(float h, float m, float n) {
+  const float a = round_to<T>(__fmul_rn(n, h));
+  const float c = round_to<T>(__fadd_rn(a, m));
+  return round_to<T>(__fmul_rn(c, __fdiv_rn(1.0f, n + 1.0f)));
 }
 
 }  // namespace pom

@@ -1,0 +1,13 @@
+// Instantiations of every PoM kernel template for element type __hip_bfloat16.
+#include "agg_impl.h"
+#include "scan_impl.h"
+#include "gate_impl.h"
+
+namespace pom {
+template hipError_t agg_fwd_t<__hip_bfloat16>(const AggParams&, hipStream_t);
+template hipError_t agg_bwd_t<__hip_bfloat16>(const AggParams&, hipStream_t);
+template hipError_t scan_fwd_t<__hip_bfloat16>(const AggParams&, const ScanParams&, hipStream_t);
+template hipError_t scan_bwd_t<__hip_bfloat16>(const ScanParams&, hipStream_t);
+template hipError_t gate_fwd_t<__hip_bfloat16>(const GateParams&, int, hipStream_t);
+template hipError_t gate_bwd_t<__hip_bfloat16>(const GateParams&, int, hipStream_t);
+}  // namespace pom

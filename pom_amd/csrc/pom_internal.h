@@ -26,68 +26,109 @@ struct RopeTables {
   int64_t pos_sn = 0;
 };
 
+// Streaming geometry shared by every token-parallel kernel.
+//
+// Channels are cut into "units": a channel (plain modes) or a rotation pair
+// (RoPE modes).  A lane owns `cpt` consecutive units (one 16-byte load of
+// bf16 per half), 2^lpr_log2 lanes cover one token row of a slab, and a
+// 256-thread workgroup streams the rows [rbeg, rend) of one chunk.
+// Tokens are grouped in F frames of L tokens; a frame is cut into cpf chunks
+// of at most RC rows, so no chunk straddles two frames.
+struct Geom {
+  int cpt = 8;
+  int lpr_log2 = 3;
+  int64_t nvec = 0;     // vector columns = units / cpt
+  int64_t nslabs = 0;   // ceil(nvec / 2^lpr_log2)
+  int64_t L = 0;        // frame length in tokens
+  int64_t F = 1;        // frame count (N = F * L)
+  int64_t RC = 0;       // rows per chunk
+  int64_t cpf = 1;      // chunks per frame = ceil(L / RC)
+  int64_t nch = 1;      // chunks per batch row = F * cpf
+};
+
 struct AggParams {
   int dtype = DT_BF16;
   int mode = MODE_PLAIN;
-  int cpt = 8;          // channels per lane (vector width)
-  int lpr_log2 = 6;     // log2(lanes per token row)
-  int K = 2;            // polynomial degree
+  int K = 2;                      // polynomial degree
+  Geom g;
 
   int64_t B = 0, N = 0, P = 0;
   const void* x = nullptr;        // (B, N, P) view, unit channel stride
   int64_t sxb = 0, sxn = 0;
-  const float* coeff = nullptr;   // (P, K)
+  const float* coeff = nullptr;   // (P, K) fp32
 
   const float* mask = nullptr;    // (B, N) weights (masked mode)
   int64_t msb = 0, msn = 0;
 
-  int64_t L = 0, NF = 1;          // frame length and frame count (N = L * NF)
-  int64_t RC = 0, nchunks = 0, cpf = 0;   // rows per chunk, chunks per row, chunks per frame
-  int64_t nvec = 0, nslabs = 0;   // lane vector columns, channel slabs
-
   RopeTables rope;
 
-  const void* carry = nullptr;    // state carry (B, P) in the element type, or null
+  const void* carry = nullptr;    // (B, P) previous running mean, element type, or null
   int64_t n_past = 0;
-  int round_carry = 1;            // round H to the element type after every frame
 
-  // forward outputs
-  void* out = nullptr;            // (B, NF, P) element type
-  float* count_out = nullptr;     // (B,) masked: sum of weights
+  // forward
+  void* out = nullptr;            // (B, F, P) element type
+  float* count_out = nullptr;     // (B,) masked: sum of the mask weights
+  int direct = 0;                 // the chunk kernel writes `out` itself (nch == 1, F == 1, no carry)
 
-  // backward inputs / outputs
-  const float* go = nullptr;      // (B, NF, P) fp32 upstream gradient
+  // backward
+  const float* go = nullptr;      // (B, F, P) fp32 upstream gradient
   const float* count_in = nullptr;
+  const float* wf = nullptr;      // (B, F, P) fp32 per-frame token weights (F > 1)
   void* gx = nullptr;             // (B, N, P) view, unit channel stride
   int64_t sgb = 0, sgn = 0;
   float* gc = nullptr;            // (P, K) fp32
 
   // workspace
-  float* partial = nullptr;
-  float* fmean = nullptr;
-  int* cnt1 = nullptr;
-  int* cnt2 = nullptr;
+  float* part = nullptr;          // forward (B, nch, P) sums | backward (B, nch, K, P)
+  float* pcnt = nullptr;          // (B, nch) masked forward: partial counts
 };
 
-hipError_t launch_agg(const AggParams& p, bool bwd, hipStream_t st);
+// Forward: chunk kernel (+ finalize unless direct).  Backward: per-frame
+// weights (F > 1), chunk kernel, coefficient-gradient finalize.
+// T is float, __hip_bfloat16 or __half; instantiated in kernels_<type>.hip.
+template <typename T> hipError_t agg_fwd_t(const AggParams& p, hipStream_t st);
+template <typename T> hipError_t agg_bwd_t(const AggParams& p, hipStream_t st);
+
+// Token-causal (prefix mean per token) aggregation as a chunked scan.
+struct ScanParams {
+  int dtype = DT_BF16;
+  int mode = MODE_PLAIN;          // PLAIN / ROPE1D / ROPE2D
+  int K = 2;
+  int cpt = 8;
+  int64_t nvec = 0;               // vector columns
+  int64_t B = 0, N = 0, P = 0;
+  int64_t RC = 0, nch = 0;        // rows per chunk, chunks per row
+
+  const void* x = nullptr;
+  int64_t sxb = 0, sxn = 0;
+  const float* coeff = nullptr;
+  RopeTables rope;
+
+  void* out = nullptr;            // (B, N, P) element type, contiguous
+  const float* go = nullptr;      // (B, N, P) fp32 contiguous upstream gradient
+  void* gx = nullptr;
+  int64_t sgb = 0, sgn = 0;
+  float* gc = nullptr;
+
+  float* csum = nullptr;          // (B, nch, P) chunk sums
+  float* part = nullptr;          // (B, nch, K, P) backward coefficient partials
+};
+
+template <typename T> hipError_t scan_fwd_t(const AggParams& chunk_sums, const ScanParams& p, hipStream_t st);
+template <typename T> hipError_t scan_bwd_t(const ScanParams& p, hipStream_t st);
 
 // Gating: sh = rot(hardsigmoid(y_s + bias)) * hagg[group(token)]
 struct GateParams {
   int dtype = DT_BF16;
   int mode = MODE_PLAIN;          // PLAIN / ROPE1D / ROPE2D
-  int cpt = 8;
-  int lpr_log2 = 6;
+  Geom g;                         // frames = hagg groups; F == N means one group per token
 
   int64_t B = 0, N = 0, P = 0;
   const void* ys = nullptr;       // (B, N, P) gate pre-activation view
   int64_t ysb = 0, ysn = 0;
-  const float* bias = nullptr;    // (P,) or null
-  const float* hagg = nullptr;    // (B, G, P) fp32
-  int64_t G = 1, Lg = 0;          // groups and tokens per group (N = G * Lg)
+  const float* bias = nullptr;    // (P,) fp32 or null
+  const void* hagg = nullptr;     // (B, G, P) element type
   RopeTables rope;
-
-  int64_t RC = 0, nchunks = 0, cpg = 0;   // rows per chunk, chunks per row, chunks per group
-  int64_t nvec = 0, nslabs = 0;
 
   void* sh = nullptr;             // (B, N, P) output view (forward)
   int64_t shb = 0, shn = 0;
@@ -99,14 +140,12 @@ struct GateParams {
   float* dhagg = nullptr;         // (B, G, P) fp32
   float* dbias = nullptr;         // (P,) fp32 or null
 
-  float* part_h = nullptr;        // (B * nchunks, P)
-  float* part_b = nullptr;        // (B * nchunks, P)
-  float* part_bb = nullptr;       // (B, P)
-  int* cnt_h = nullptr;           // (B * G * nslabs)
-  int* cnt_b1 = nullptr;          // (B * nslabs)
-  int* cnt_b2 = nullptr;          // (nslabs)
+  float* part_h = nullptr;        // (B, nch, P)
+  float* part_b = nullptr;        // (B, nch, P)
 };
 
-hipError_t launch_gate(const GateParams& p, bool bwd, hipStream_t st);
+// per_token: hagg holds one row per token (token-causal aggregation).
+template <typename T> hipError_t gate_fwd_t(const GateParams& p, int per_token, hipStream_t st);
+template <typename T> hipError_t gate_bwd_t(const GateParams& p, int per_token, hipStream_t st);
 
 }  // namespace pom

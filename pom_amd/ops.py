@@ -81,9 +81,7 @@ def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     count = torch.empty(B, dtype=torch.float32, device=x.device) if mask32 is not None else None
     rk = rope.kind if rope is not None else _lib.ROPE_NONE
     nbytes = lib.pom_agg_workspace_size(dt, B, N, P, k, frame_len, rk, 0)
-    if nbytes == 0:
-        nbytes = _lib.COUNTER_BYTES   # invalid shape: the launch below reports why
-    ws = workspace(x.device, nbytes)
+    ws = workspace(x.device, nbytes)   # a zero size (invalid shape) is reported by the launch
     xv = view3(x)
     if carry is not None:
         carry = carry.reshape(B, P).contiguous()
@@ -109,10 +107,10 @@ def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     dt = dtype_code(x)
     gc = torch.empty(P, k, dtype=torch.float32, device=x.device)
     rk = rope.kind if rope is not None else _lib.ROPE_NONE
-    nbytes = lib.pom_agg_workspace_size(dt, B, N, P, k, frame_len, rk, 1) or _lib.COUNTER_BYTES
+    nbytes = lib.pom_agg_workspace_size(dt, B, N, P, k, frame_len, rk, 1)
     ws = workspace(x.device, nbytes)
     xv, gv = view3(x), view3(grad_x)
-    go32 = go32.contiguous()
+    go32 = go32.float().contiguous()
     with _Span("agg_bwd"):
         rc = lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
                              mask32.stride(0) if mask32 is not None else 0,
@@ -123,37 +121,46 @@ def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     return gc
 
 
-def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg32: torch.Tensor,
+def _hagg(hagg: torch.Tensor, ys: torch.Tensor) -> torch.Tensor:
+    """The gate reads the aggregate in the element type of y_s, contiguous."""
+    if hagg.dtype != ys.dtype:
+        hagg = hagg.to(ys.dtype)
+    return hagg.contiguous()
+
+
+def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.Tensor,
                  rope: Optional[RopeSpec] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sh = R hardsigmoid(ys + bias) * hagg[group], via pom_gate_fwd."""
     lib = _lib.load()
     B, N, P = ys.shape
-    G = hagg32.shape[1]
+    hagg = _hagg(hagg, ys)
+    G = hagg.shape[1]
     sh = torch.empty(B, N, P, dtype=ys.dtype, device=ys.device) if out is None else out
     yv, sv = view3(ys), view3(sh)
     with _Span("gate_fwd"):
-        rc = lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G,
+        rc = lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
                               rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
     check(rc, "pom_gate_fwd")
     return sh
 
 
-def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg32: torch.Tensor,
+def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.Tensor,
                   grad_sh: torch.Tensor, grad_ys: torch.Tensor, rope: Optional[RopeSpec] = None,
                   want_bias: bool = True):
     """Writes grad_ys in place; returns (grad_hagg (B, G, P) fp32, grad_bias (P,) fp32 or None)."""
     lib = _lib.load()
     B, N, P = ys.shape
-    G = hagg32.shape[1]
+    hagg = _hagg(hagg, ys)
+    G = hagg.shape[1]
     dt = dtype_code(ys)
     gh = torch.empty(B, G, P, dtype=torch.float32, device=ys.device)
     gb = torch.empty(P, dtype=torch.float32, device=ys.device) if want_bias else None
     rk = rope.kind if rope is not None else _lib.ROPE_NONE
-    nbytes = lib.pom_gate_workspace_size(dt, B, N, P, G, rk) or _lib.COUNTER_BYTES
+    nbytes = lib.pom_gate_workspace_size(dt, B, N, P, G, rk)
     ws = workspace(ys.device, nbytes)
     yv, gv, dv = view3(ys), view3(grad_sh), view3(grad_ys)
     with _Span("gate_bwd"):
-        rc = lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg32.data_ptr(), G,
+        rc = lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
                               rope_ptr(rope), ctypes.byref(gv), ctypes.byref(dv), gh.data_ptr(), ptr(gb),
                               ws.data_ptr(), ws.numel(), stream_handle(ys.device))
     check(rc, "pom_gate_bwd")
@@ -267,9 +274,9 @@ class _Gate(torch.autograd.Function):
         _lib.require_device(ys, hagg)
         B, N, P = ys.shape
         b32 = None if bias is None else bias.detach().float().contiguous()
-        h32 = hagg.detach().float().contiguous()
-        sh = gate_forward(ys, b32, h32, rope)
-        ctx.save_for_backward(ys, b32, h32)
+        h = _hagg(hagg.detach(), ys)
+        sh = gate_forward(ys, b32, h, rope)
+        ctx.save_for_backward(ys, b32, h)
         ctx.rope = rope
         ctx.bias_dtype = None if bias is None else bias.dtype
         ctx.hagg_dtype = hagg.dtype
@@ -277,9 +284,9 @@ class _Gate(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_sh):
-        ys, b32, h32 = ctx.saved_tensors
+        ys, b32, h = ctx.saved_tensors
         gys = torch.empty_like(ys, memory_format=torch.contiguous_format)
-        gh, gb = gate_backward(ys, b32, h32, grad_sh, gys, ctx.rope, want_bias=b32 is not None)
+        gh, gb = gate_backward(ys, b32, h, grad_sh, gys, ctx.rope, want_bias=b32 is not None)
         return (gys, None if gb is None else gb.to(ctx.bias_dtype), gh.to(ctx.hagg_dtype), None)
 
 
@@ -321,15 +328,14 @@ class _PoMLayer(torch.autograd.Function):
         h_view, s_view = y3[..., :P], y3[..., P:]
         c32 = _coeff32(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
-        h32 = hagg.float()
         b32 = se_bias.detach().float().contiguous()
-        sh = gate_forward(s_view, b32, h32, rope_s)                 # (B, N, P)
+        sh = gate_forward(s_view, b32, hagg, rope_s)                # (B, N, P)
         wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
         with _Span("gemm_ag_fwd"):
             out = torch.mm(sh.view(B * N, P), wa.t())
         if b_ag is not None:
             out = out + b_ag.to(dt)
-        ctx.save_for_backward(x, y, sh, h32, c32, b32, wq, wa, mask, count)
+        ctx.save_for_backward(x, y, sh, hagg, c32, b32, wq, wa, mask, count)
         ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None)
         ctx.dtypes = (w_qc.dtype, se_bias.dtype, coeff.dtype, w_ag.dtype,
                       None if b_ag is None else b_ag.dtype)
@@ -337,7 +343,7 @@ class _PoMLayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out, grad_hagg):
-        x, y, sh, h32, c32, b32, wq, wa, mask, count = ctx.saved_tensors
+        x, y, sh, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
         k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias = ctx.meta
         B, N, D = x.shape
         P = c32.shape[0]
@@ -354,7 +360,7 @@ class _PoMLayer(torch.autograd.Function):
         y3 = y.view(B, N, 2 * P)
         dy = torch.empty(T, 2 * P, dtype=dt, device=x.device)
         dy3 = dy.view(B, N, 2 * P)
-        dh, dbias = gate_backward(y3[..., P:], b32, h32, dsh.view(B, N, P), dy3[..., P:], rope_s)
+        dh, dbias = gate_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), dy3[..., P:], rope_s)
         if grad_hagg is not None:
             dh = dh + grad_hagg.float()
         dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h)
