@@ -18,6 +18,9 @@ Pinning (how each function is checked, see tests/test_oracle.py):
   agg_block_causal              frame_len=N == mean; frame_len=1 == causal;
                                 equals the dense 3-D block mask of the reference
   frame_loop (state_forward)    == full block-causal for equal frames
+  running_mean_frames           the reference's state_forward arithmetic on bf16
+                                tensors (CPU torch, division differences
+                                bounded) and, on the GPU box, bit for bit
   rope tables / apply_rope_*    closed-form angle of one pair; positions 0 ==
                                 identity; rotation preserves pair norms
   PoM / PoMRoPE composition     golden fixtures written by the reference itself
@@ -39,7 +42,7 @@ __all__ = [
     "hardsigmoid", "precompute_freqs_1d", "precompute_freqs_2d",
     "apply_rope_1d", "apply_rope_2d", "OracleParams", "init_params",
     "get_h_s", "pom_forward", "state_forward", "rope_forward",
-    "block_causal_dense_mask",
+    "block_causal_dense_mask", "running_mean_frames",
 ]
 
 
@@ -251,6 +254,11 @@ class OracleParams:
     w_ag: torch.Tensor          # (D, P)
     b_ag: Optional[torch.Tensor]
     rope: Optional[dict] = None  # tables for PoMRoPE
+    n_groups: int = 1
+    po_w: Optional[torch.Tensor] = None   # n_groups > 1: Conv1d weight (P, D / G, 1)
+    po_b: Optional[torch.Tensor] = None
+    se_w: Optional[torch.Tensor] = None   # n_groups > 1: se_proj Linear (S, D) with bias
+    se_b: Optional[torch.Tensor] = None
 
     @property
     def po_dim(self) -> int:
@@ -266,7 +274,8 @@ class OracleParams:
                                                for k, v in self.rope.items()}
         return OracleParams(self.dim, self.degree, self.expand, self.n_sel_heads,
                             cv(self.w_qc), cv(self.se_bias), cv(self.po_coeff),
-                            cv(self.w_ag), cv(self.b_ag), rope)
+                            cv(self.w_ag), cv(self.b_ag), rope, self.n_groups,
+                            cv(self.po_w), cv(self.po_b), cv(self.se_w), cv(self.se_b))
 
 
 def init_params(dim: int, degree: int, expand: int, n_sel_heads: int = 1, bias: bool = False,
@@ -298,6 +307,9 @@ def init_params(dim: int, degree: int, expand: int, n_sel_heads: int = 1, bias: 
 def get_h_s(prm: OracleParams, xq: torch.Tensor, xc: torch.Tensor, self_mixing: bool = True):
     """Projected context h and hardsigmoid gate s — pom/pom.py:193-214."""
     p = prm.po_dim
+    if prm.n_groups > 1:
+        h = F.conv1d(xc.transpose(1, 2), prm.po_w, prm.po_b, groups=prm.n_groups).transpose(1, 2)
+        return h, hardsigmoid(F.linear(xq, prm.se_w, prm.se_b))
     if self_mixing:
         y = F.linear(xq, prm.w_qc)
         return y[..., :p], hardsigmoid(y[..., p:] + prm.se_bias)
@@ -340,6 +352,35 @@ def state_forward(prm: OracleParams, xq: torch.Tensor, xc: Optional[torch.Tensor
         h, n_past = h_cur, 0
     out = _out_proj(prm, selection(s, h, prm.n_sel_heads))
     return out, {"h": h, "n": n_past + n_cur}
+
+
+def running_mean_frames(means: torch.Tensor, dtype, carry: Optional[torch.Tensor] = None,
+                        n_past: int = 0) -> torch.Tensor:
+    """The carry of a PoM.state_forward loop (pom/pom.py:255-259) over frames.
+
+    ``means`` (B, F, P) holds the per-call means; each is a tensor of ``dtype``
+    in the reference (pom/pom_triton.py:348).  Every step is evaluated the way
+    torch's GPU kernels evaluate ``(n * h + 1 * m) / (n + 1)`` on ``dtype``
+    tensors: each op computes in fp32 and rounds to ``dtype``, and dividing by
+    the int ``n + 1`` multiplies by its fp32 reciprocal (ATen's true-divide
+    kernel with a host-scalar divisor).  Returns (B, F, P) in ``dtype``.
+    """
+    out = []
+    h = None if carry is None else carry.to(dtype)
+    n = n_past
+    one = torch.tensor(1.0, dtype=torch.float32)
+    for f in range(means.shape[1]):
+        m = means[:, f].to(dtype)
+        if h is None:
+            h = m
+        else:
+            a = (h.float() * float(n)).to(dtype)
+            c = (a.float() + m.float()).to(dtype)
+            inv = one / torch.tensor(float(n + 1), dtype=torch.float32)
+            h = (c.float() * inv).to(dtype)
+        out.append(h)
+        n += 1
+    return torch.stack(out, dim=1)
 
 
 def _rope(prm: OracleParams, x: torch.Tensor, positions, positions_hw):

@@ -1,0 +1,171 @@
+"""CPU tests of the C ABI (include/pom_amd.h) and of the host-side module logic.
+
+The library is loaded and every declared symbol is bound; argument
+validation is exercised with calls that fail before anything touches a GPU
+(no kernel is launched without one).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pom_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pom_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from pom_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libpom_amd.so not built (python pom_amd/csrc/build.py)")
+    return _lib.load()
+
+
+def test_header_lists_expected_entry_points():
+    names = _declared_functions()
+    for n in ["pom_abi_version", "pom_last_error", "pom_agg_workspace_size", "pom_agg_fwd", "pom_agg_bwd",
+              "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd"]:
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    from pom_amd import _lib
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in include/pom_amd.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature in pom_amd/_lib.py"
+    assert lib.pom_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_sizes(lib):
+    # valid shapes report a positive size; invalid ones report 0
+    assert lib.pom_agg_workspace_size(1, 16, 1024, 2304, 2, 1024, 0, 0) > 0
+    assert lib.pom_agg_workspace_size(1, 16, 1024, 2304, 2, 1024, 0, 1) > 0
+    assert lib.pom_agg_workspace_size(1, 4, 16384, 4096, 2, 1024, 0, 1) > 0
+    assert lib.pom_agg_workspace_size(1, 4, 16384, 4096, 2, 1, 0, 1) > 0       # token-causal
+    assert lib.pom_agg_workspace_size(1, 16, 1024, 2304, 17, 1024, 0, 0) == 0  # degree > 16
+    assert lib.pom_agg_workspace_size(1, 16, 1000, 2304, 2, 64, 0, 0) == 0     # frame_len must divide N
+    assert lib.pom_agg_workspace_size(7, 16, 1024, 2304, 2, 1024, 0, 0) == 0   # bad dtype
+    assert lib.pom_gate_workspace_size(1, 16, 1024, 2304, 1, 0) > 0
+    assert lib.pom_gate_workspace_size(1, 16, 1024, 2304, 3, 0) == 0           # groups must divide N
+    # the size depends only on the shape: larger shapes never need less
+    a = lib.pom_agg_workspace_size(1, 8, 1024, 2304, 2, 1024, 0, 1)
+    b = lib.pom_agg_workspace_size(1, 16, 1024, 2304, 2, 1024, 0, 1)
+    assert b >= a
+
+
+def _view(ptr=256, sb=0, sn=0):
+    from pom_amd._lib import PomView
+    return PomView(ptr, sb, sn)
+
+
+def test_validation_errors_before_launch(lib):
+    from pom_amd import _lib
+    x = _view(256, 1024 * 64, 64)
+    coeff = ctypes.c_void_p(512)
+    out = ctypes.c_void_p(1024)
+    ws = ctypes.c_void_p(4096)
+    # empty shape
+    rc = lib.pom_agg_fwd(1, 0, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID and b"empty shape" in lib.pom_last_error()
+    # degree out of range
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 0, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_UNSUPPORTED
+    # frame_len not dividing N
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 5, None, 0, None, out, None,
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID and b"frame_len" in lib.pom_last_error()
+    # null coefficients / output
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), None, None, 0, 0, 16, None, 0, None, out, None,
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, None, None,
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID
+    # workspace missing or too small
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+                         None, 0, None)
+    assert rc == _lib.POM_ERR_WORKSPACE
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+                         ws, 16, None)
+    assert rc == _lib.POM_ERR_WORKSPACE
+    # masked forward without count_out; masked with frames
+    mask = ctypes.c_void_p(2048)
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, mask, 16, 1, 16, None, 0, None, out, None,
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, mask, 16, 1, 8, None, 0, None, out,
+                         ctypes.c_void_p(4096), ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_UNSUPPORTED
+    # carry with n_past < 1
+    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, ctypes.c_void_p(8192), 0,
+                         None, out, None, ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID
+    # RoPE with an odd channel count
+    rope = _lib.PomRope(_lib.ROPE_1D, 512, 512, None, None, 32, 16, 0, 512, 1)
+    rc = lib.pom_agg_fwd(1, 2, 16, 63, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, ctypes.byref(rope),
+                         out, None, ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID and b"even" in lib.pom_last_error()
+    # gate: groups not dividing N
+    rc = lib.pom_gate_fwd(1, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 3, None,
+                          ctypes.byref(_view(4096, 1024, 64)), None)
+    assert rc == _lib.POM_ERR_INVALID
+
+
+def test_python_errors_without_gpu():
+    import pom_amd
+    m = pom_amd.PoM(16, 2, 2)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        m(torch.randn(1, 4, 16))
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        pom_amd.poly_agg_mean_hip(torch.randn(1, 4, 16), torch.randn(16, 2), 2)
+
+
+def test_degree_and_mask_validation():
+    import importlib
+    import pom_amd
+    from pom_amd import ops
+    pm = importlib.import_module("pom_amd.pom")
+    with pytest.raises(NotImplementedError):
+        ops._check_degree(17)
+    with pytest.raises(ValueError):
+        ops._check_degree(0)
+    with pytest.raises(ValueError):
+        pm._frame_len_of(("block_causal", 5), 16)
+    assert pm._frame_len_of(pom_amd.block_causal(4), 16) == 4
+
+
+def test_module_parameters_match_reference_names_and_init():
+    """Same parameter names, shapes and RNG draw order as pom/pom.py:180-191,
+    checked against the oracle's init_params (pinned by the golden fixtures)."""
+    import pom_amd
+    from oracle import pom_oracle as O
+    torch.manual_seed(0)
+    m = pom_amd.PoM(32, 3, 2)
+    torch.manual_seed(0)
+    prm = O.init_params(32, 3, 2)
+    names = sorted(n for n, _ in m.named_parameters())
+    assert names == ["ag_proj.weight", "po_coeff", "qc_proj.weight", "se_bias"]
+    assert torch.equal(m.qc_proj.weight, prm.w_qc) and torch.equal(m.po_coeff, prm.po_coeff)
+    assert torch.equal(m.ag_proj.weight, prm.w_ag) and torch.equal(m.se_bias, prm.se_bias)
+    mh = pom_amd.PoM(32, 2, 2, 1, 4)
+    assert mh.qc_proj.weight.shape == (64 + 4, 32) and mh.se_bias.shape == (4,)
+    mg = pom_amd.PoM(32, 2, 2, 4, 1, True)
+    assert sorted(n for n, _ in mg.named_parameters()) == sorted(
+        ["po_proj.weight", "po_proj.bias", "se_proj.weight", "se_proj.bias", "po_coeff", "ag_proj.weight",
+         "ag_proj.bias"])
+    r = pom_amd.PoMRoPE(32, 2, 2, rope_2d=True)
+    assert sorted(n for n, _ in r.named_buffers()) == ["col_cos", "col_sin", "row_cos", "row_sin"]
+    assert r.row_cos.shape == (64, 16)
+    sd = r.state_dict()
+    r2 = pom_amd.PoMRoPE(32, 2, 2, rope_2d=True)
+    r2.load_state_dict(sd, strict=True)
