@@ -223,13 +223,16 @@ __device__ __forceinline__ float xor_sum_rows(float v, int lo_bits) {
 //   c = T(a + m)              (the n_current = 1 term is m itself)
 //   h = T(c * fp32(1/(n+1)))  (division by a scalar is a multiply by its
 //                              fp32 reciprocal in torch's GPU kernels)
-// The _rn intrinsics keep the compiler from contracting into an fma.
+// Contraction is off in this function: an fma of n * h + m would round once
+// where the reference rounds twice.
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ float running_mean_step(float h, float m, float n) {
-  const float a = round_to<T>(__fmul_rn(n, h));
-  const float c = round_to<T>(__fadd_rn(a, m));
-  return round_to<T>(__fmul_rn(c, __fdiv_rn(1.0f, n + 1.0f)));
+#pragma clang fp contract(off)
+  const float a = round_to<T>(n * h);
+  const float c = round_to<T>(a + m);
+  const float inv = 1.0f / (n + 1.0f);   // correctly rounded (no fast-math)
+  return round_to<T>(c * inv);
 }
 
 }  // namespace pom
