@@ -25,6 +25,7 @@ import torch
 
 from . import _lib
 from ._lib import RopeSpec, check, dtype_code, ptr, rope_ptr, view3, workspace, stream_handle
+from .gemm_select import tuned_gemms
 
 
 # Optional per-launch timing: when ``kernel_timer`` is a list, every launch
@@ -322,7 +323,7 @@ class _PoMLayer(torch.autograd.Function):
         dt = x.dtype
         x2 = x.reshape(B * N, D)
         wq = w_qc if w_qc.dtype == dt else w_qc.to(dt)
-        with _Span("gemm_qc_fwd"):
+        with _Span("gemm_qc_fwd"), tuned_gemms():
             y = torch.mm(x2, wq.t())                                # (T, 2P)
         y3 = y.view(B, N, 2 * P)
         h_view, s_view = y3[..., :P], y3[..., P:]
@@ -331,7 +332,7 @@ class _PoMLayer(torch.autograd.Function):
         b32 = se_bias.detach().float().contiguous()
         sh = gate_forward(s_view, b32, hagg, rope_s)                # (B, N, P)
         wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
-        with _Span("gemm_ag_fwd"):
+        with _Span("gemm_ag_fwd"), tuned_gemms():
             out = torch.mm(sh.view(B * N, P), wa.t())
         if b_ag is not None:
             out = out + b_ag.to(dt)
@@ -352,9 +353,9 @@ class _PoMLayer(torch.autograd.Function):
         g2 = grad_out.reshape(T, D)
         if g2.dtype != dt:
             g2 = g2.to(dt)
-        with _Span("gemm_ag_dgrad"):
+        with _Span("gemm_ag_dgrad"), tuned_gemms():
             dsh = torch.mm(g2, wa)                                  # (T, P)
-        with _Span("gemm_ag_wgrad"):
+        with _Span("gemm_ag_wgrad"), tuned_gemms():
             dw_ag = torch.mm(g2.t(), sh.view(T, P))                 # (D, P)
         db_ag = g2.float().sum(0) if has_bias else None
         y3 = y.view(B, N, 2 * P)
@@ -364,9 +365,9 @@ class _PoMLayer(torch.autograd.Function):
         if grad_hagg is not None:
             dh = dh + grad_hagg.float()
         dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h)
-        with _Span("gemm_qc_dgrad"):
+        with _Span("gemm_qc_dgrad"), tuned_gemms():
             dx = torch.mm(dy, wq)                                   # (T, D)
-        with _Span("gemm_qc_wgrad"):
+        with _Span("gemm_qc_wgrad"), tuned_gemms():
             dw_qc = torch.mm(dy.t(), x.reshape(T, D))               # (2P, D)
         g_carry = None
         if has_carry:

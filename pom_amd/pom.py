@@ -14,7 +14,8 @@ Mask forms accepted by ``forward`` / ``polynomial_aggregation_``:
                                 from polynomial_aggregation_; expanded per token
                                 inside the module.  Equivalent to the reference's
                                 dense block-lower-triangular (B, N, N) mask.
-  (B, M, N) tensor              not supported by the kernels (NotImplementedError)
+  (B, M, N) tensor              dense cross mask (pom/pom.py:41-45) as a batched GEMM
+                                on the GPU (dense.full_mask_mix)                 -> (B, M, P)
 """
 from __future__ import annotations
 
@@ -24,7 +25,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops
+from . import dense, ops
 from ._lib import require_device
 
 __all__ = ["PoM", "pom", "pom_activation", "polynomial_aggregation_", "polynomial_selection_",
@@ -71,8 +72,7 @@ def polynomial_aggregation_(x: torch.Tensor, coeff: torch.Tensor, k: int, mask=N
         if mask.dim() == 2:
             return ops.poly_agg_masked_hip(x, mask, coeff, k)
         if mask.dim() == 3:
-            raise NotImplementedError("pom_amd: dense (B, M, N) masks are not supported; use "
-                                      "\"causal\", a (B, N) mask or pom_amd.block_causal(frame_len)")
+            return dense.full_mask_mix(dense.poly_features(x, coeff, k), mask)
     raise ValueError(f'Unsupported mask: expected None, "causal", or a 2/3-D tensor.')
 
 
@@ -133,35 +133,54 @@ class PoM(nn.Module):
     def _fused_ok(self, xq, xc) -> bool:
         return self.n_groups == 1 and self.n_sel_heads <= 1 and xq is xc
 
-    def _check_supported(self):
-        if self.n_sel_heads > 1:
-            raise NotImplementedError("pom_amd: n_sel_heads > 1 gating is not supported yet")
-
     def _h_and_gate_input(self, xq, xc):
-        """Context projection h and gate pre-activation (without se_bias) for the
-        unfused routes — pom/pom.py:201-213."""
+        """Context projection h and gate pre-activation y_s (without se_bias) —
+        pom/pom.py:201-213: one GEMM for self-mixing, sliced into [h | y_s]."""
         if self.n_groups > 1:
-            h = self.po_proj(xc.transpose(1, 2)).transpose(1, 2)
+            # grouped 1x1 convolution over channels; its output is channel-strided
+            h = self.po_proj(xc.transpose(1, 2)).transpose(1, 2).contiguous()
             return h, F.linear(xq, self.se_proj.weight), self.se_proj.bias
         w = self.qc_proj.weight
+        if xq is xc:
+            y = F.linear(xq, w)
+            return y[..., :self._po_dim], y[..., self._po_dim:], self.se_bias
         return F.linear(xc, w[:self._po_dim]), F.linear(xq, w[self._po_dim:]), self.se_bias
 
-    def _mix(self, xq, xc, mask, frame_len, rope_h=None, rope_s=None):
-        """Unfused route: projections, HIP aggregation, HIP gating."""
-        h, ys, bias = self._h_and_gate_input(xq, xc)
-        if mask is not None and not isinstance(mask, (str, tuple)) and mask.dim() == 3:
-            polynomial_aggregation_(h, self.po_coeff, self.order, mask)   # raises
-        if frame_len is not None:
-            h_agg = ops._PolyAgg.apply(h, self.po_coeff, self.order, frame_len, None, rope_h, None, 0)
-        elif isinstance(mask, torch.Tensor):
+    def _aggregate(self, h, mask, frame_len, rope_h=None, rot_h=None):
+        """h_agg of the projected context for every mask form (RoPE: rope_h is the
+        kernel's table description, rot_h the same rotation as a tensor op)."""
+        k = self.order
+        if isinstance(mask, torch.Tensor) and mask.dim() == 3:
+            p = dense.poly_features(h, self.po_coeff, k)
+            return dense.full_mask_mix(rot_h(p) if rot_h is not None else p, mask)
+        if isinstance(mask, torch.Tensor) and mask.dim() == 2:
             if rope_h is not None:
-                raise NotImplementedError("pom_amd: RoPE with a (B, N) mask is not supported yet")
-            h_agg = ops.poly_agg_masked_hip(h, mask, self.po_coeff, self.order)
-        else:
-            h_agg = ops._PolyAgg.apply(h, self.po_coeff, self.order, h.shape[1], None, rope_h, None, 0)
-        if h_agg.shape[1] not in (1,) and ys.shape[1] % h_agg.shape[1]:
+                return dense.masked_mean(rot_h(dense.poly_features(h, self.po_coeff, k)), mask)
+            return ops.poly_agg_masked_hip(h, mask, self.po_coeff, k)
+        fl = h.shape[1] if frame_len is None else frame_len
+        return ops._PolyAgg.apply(h, self.po_coeff, k, fl, None, rope_h, None, 0)
+
+    def _select(self, ys, bias, h_agg, rope_s=None, rot_s=None):
+        """Gate + selection — pom/pom.py:207 and :103-122 (query-side RoPE
+        pom/pom_rope.py:522).  One HIP kernel for n_sel_heads <= 1; per-head
+        scalar gates as tensor ops otherwise."""
+        T, G = ys.shape[1], h_agg.shape[1]
+        if G not in (1, T) and T % G:
             raise ValueError("query length must be a multiple of the aggregate's group count")
-        return self.ag_proj(ops.gate_hip(ys, bias, h_agg, rope_s))
+        if self.n_sel_heads > 1:
+            s = F.hardsigmoid(ys + bias)
+            if rot_s is not None:
+                s = rot_s(s)
+            if G not in (1, T):
+                h_agg = h_agg.repeat_interleave(T // G, dim=1)
+            return polynomial_selection_(s, h_agg, self.n_sel_heads)
+        return ops.gate_hip(ys, bias, h_agg, rope_s)
+
+    def _mix(self, xq, xc, mask, frame_len, rope_h=None, rope_s=None, rot_h=None, rot_s=None):
+        """Unfused route: projections, aggregation, gating, out-projection."""
+        h, ys, bias = self._h_and_gate_input(xq, xc)
+        h_agg = self._aggregate(h, mask, frame_len, rope_h, rot_h)
+        return self.ag_proj(self._select(ys, bias, h_agg, rope_s, rot_s))
 
     def _frame_len(self, mask, n: int) -> Optional[int]:
         if mask is None:
@@ -177,7 +196,6 @@ class PoM(nn.Module):
         if xc is None:
             xc = xq
         require_device(xq, xc)
-        self._check_supported()
         fl = self._frame_len(mask, xc.shape[1])
         if self._fused_ok(xq, xc) and (fl is not None or mask is None or
                                         (isinstance(mask, torch.Tensor) and mask.dim() == 2)):
@@ -197,7 +215,6 @@ class PoM(nn.Module):
         if xc is None:
             xc = xq
         require_device(xq, xc)
-        self._check_supported()
         carry = None if state is None else state["h"]
         n_past = 0 if state is None else int(state["n"])
         if n_past == 0:
@@ -212,17 +229,16 @@ class PoM(nn.Module):
             return out, {"h": h, "n": n_past + 1}
         h_raw, ys, bias = self._h_and_gate_input(xq, xc)
         h = ops.poly_agg_state_hip(h_raw, self.po_coeff, self.order, carry, n_past)
-        return self.ag_proj(ops.gate_hip(ys, bias, h)), {"h": h, "n": n_past + 1}
+        return self.ag_proj(self._select(ys, bias, h)), {"h": h, "n": n_past + 1}
 
     @torch.no_grad()
     def ar_forward(self, xq: torch.Tensor, state: Dict[str, Any]) -> Tuple[torch.Tensor, Dict[str, Any]]:
         """Autoregressive forward without aggregation — pom/pom.py:264-275: the gate
         multiplies the raw projected context token by token."""
         require_device(xq)
-        self._check_supported()
         B, T, D = xq.shape
         h, ys, bias = self._h_and_gate_input(xq, xq)
-        out = self.ag_proj(ops.gate_hip(ys, bias, h))
+        out = self.ag_proj(self._select(ys, bias, h))
         return out, {"max_len": state["max_len"], "h": h, "n": state["n"] + T}
 
     def reset(self, state: Dict[str, Any]) -> Dict[str, Any]:

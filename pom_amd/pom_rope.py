@@ -102,26 +102,49 @@ class PoMRoPE(PoM):
             raise ValueError(f"positions must have shape ({n},), got {tuple(positions.shape)}")
         return RopeSpec(_lib.ROPE_1D, [self.freqs_cos, self.freqs_sin], positions.to(device))
 
+    def _rope_torch(self, x: torch.Tensor, positions, positions_hw) -> torch.Tensor:
+        """PoMRoPE._rope — pom/pom_rope.py:386-437 as tensor ops: full-width
+        tables for P channels, tables strided by head_dim (2-D) or head_dim / 2
+        (1-D) for the n_sel_heads-channel gate."""
+        n, d = x.shape[1], x.shape[-1]
+        if self.rope_2d:
+            if positions_hw is None:
+                raise ValueError("positions_hw (N, 2) must be provided when rope_2d=True")
+            pos = positions_hw.to(x.device)
+            if d == self._po_dim:
+                return apply_rope_2d(x, pos, self.row_cos, self.row_sin, self.col_cos, self.col_sin)
+            st, q = self.head_dim, d // 4
+            return apply_rope_2d(x, pos, self.row_cos[:, ::st][:, :q], self.row_sin[:, ::st][:, :q],
+                                 self.col_cos[:, ::st][:, :q], self.col_sin[:, ::st][:, :q])
+        pos = torch.arange(n, device=x.device) if positions is None else positions.to(x.device)
+        if d == self._po_dim:
+            return apply_rope_1d(x, pos, self.freqs_cos, self.freqs_sin)
+        st, half = self.head_dim // 2, d // 2
+        return apply_rope_1d(x, pos, self.freqs_cos[:, ::st][:, :half], self.freqs_sin[:, ::st][:, :half])
+
     def forward(self, xq: torch.Tensor, xc: Optional[torch.Tensor] = None, mask=None,
                 positions: Optional[torch.Tensor] = None, ctx_positions: Optional[torch.Tensor] = None,
                 positions_hw: Optional[torch.Tensor] = None,
                 ctx_positions_hw: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """pom/pom_rope.py:443-526."""
+        """pom/pom_rope.py:443-526.  Context features are rotated before they are
+        aggregated (inside the aggregation kernel), the query gate after the
+        hardsigmoid (inside the gating kernel, or as tensor ops for
+        n_sel_heads > 1)."""
         self_mixing = xc is None or xc is xq
         if xc is None:
             xc = xq
         require_device(xq, xc)
-        self._check_supported()
         eff_ctx = ctx_positions if ctx_positions is not None else (positions if self_mixing else None)
         eff_ctx_hw = ctx_positions_hw if ctx_positions_hw is not None else (positions_hw if self_mixing else None)
         rope_h = self._spec(xc.shape[1], eff_ctx, eff_ctx_hw, xc.device)
-        rope_s = self._spec(xq.shape[1], positions, positions_hw, xq.device)
+        rot_h = lambda t: self._rope_torch(t, eff_ctx, eff_ctx_hw)
+        rot_s = lambda t: self._rope_torch(t, positions, positions_hw)
         fl = self._frame_len(mask, xc.shape[1])
-        if isinstance(mask, torch.Tensor) and mask.dim() == 2:
-            raise NotImplementedError("pom_amd: RoPE with a (B, N) mask is not supported yet")
         if self._fused_ok(xq, xc) and (mask is None or fl is not None):
+            rope_s = self._spec(xq.shape[1], positions, positions_hw, xq.device)
             out, _ = ops.pom_layer(xq, self.qc_proj.weight, self.se_bias, self.po_coeff,
                                    self.ag_proj.weight, self.ag_proj.bias, self.order, fl, None,
                                    rope_h, rope_s)
             return out
-        return self._mix(xq, xc, mask, fl, rope_h, rope_s)
+        rope_s = None if self.n_sel_heads > 1 else self._spec(xq.shape[1], positions, positions_hw, xq.device)
+        return self._mix(xq, xc, mask, fl, rope_h, rope_s, rot_h, rot_s)
