@@ -9,9 +9,11 @@ input that is resident in HBM before the timed region starts (x, upstream
 gradient and weights).  The default workload is config 2 of the baseline
 (image-DiT layer: B=16, N=1024, D=1152, degree 2, expand 2, bf16).  Every
 launch of the layer (six projection GEMMs, aggregation and gating kernels) is
-bracketed by HIP events on the launch stream inside the timed region, giving
-each kernel's average duration; the roofline object reports the kernel that
-takes the most time per step, and "kernels" reports all of them.
+bracketed by HIP events on its launch stream in a second, instrumented pass
+of the same K steps (events cost ~5 % of a step, so the headline pass runs
+without them), giving each kernel's average duration; the roofline object
+reports the kernel that takes the most time per step, and "kernels" reports
+all of them.
 
 The CPU baseline runs the oracle (a pure-PyTorch restatement of the reference
 path) in fp32 on the host cores on a bounded sample of the same workload.
@@ -57,6 +59,12 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-launch events")
+    ap.add_argument("--graph", action="store_true",
+                    help="capture one forward+backward step in a HIP graph and time its replays "
+                         "(host launch overhead removed); per-kernel events are not available then")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"),
+                    help="turn four rocprofv3 --pmc databases (FETCH_SIZE and WRITE_SIZE of a bench run and "
+                         "of a --copy-calib run) into per-kernel HBM traffic; writes profiles/traffic_<config>.json")
     ap.add_argument("--copy-calib", type=float, default=0.0,
                     help="instead of the layer, run a plain device copy of this many MiB "
                          "(calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -151,7 +159,7 @@ def kernel_work(cfg, extra):
 # GPU leg
 # ---------------------------------------------------------------------------
 
-def gpu_run(cfg, steps, warmup, kernel_timing):
+def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
     import torch
     from pom_amd import ops, _lib
     _lib.load()
@@ -175,20 +183,64 @@ def gpu_run(cfg, steps, warmup, kernel_timing):
         step()
     torch.cuda.synchronize()
 
+    if graph:
+        # capture one step on a side stream (torch's recipe), then replay it
+        for p in params:
+            p.grad = None
+        xd.grad = None
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        for p in params:
+            p.grad = None
+        xd.grad = None
+        with torch.cuda.graph(g):
+            out = fwd(m, xd)
+            out.backward(god)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            g.replay()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        return (t1 - t0) / steps * 1e3, None, {}, extra, (None, None)
+
+    # instrumented pass: K steps with HIP events around every launch group on
+    # its launch stream -> per-kernel durations and the dominant kernel
+    per = {}
+    dominant = None
+    if kernel_timing:
+        ops.kernel_timer = []
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        for name, s, e in ops.kernel_timer:
+            per.setdefault(name, []).append(s.elapsed_time(e) * 1e-3)   # seconds
+        dominant = max(per, key=lambda k: sum(per[k]))
+        # the timed region records events around the dominant kernel only
+        # (events around every launch would add ~5 % to the step)
+        ops.kernel_timer = []
+        ops.kernel_timer_only = {dominant}
+
     # timed region: K fwd+bwd steps
-    ops.kernel_timer = [] if kernel_timing else None
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    spans = ops.kernel_timer or []
-    ops.kernel_timer = None
-    per = {}
-    for name, s, e in spans:
-        per.setdefault(name, []).append(s.elapsed_time(e) * 1e-3)   # seconds
     ms_step = (t1 - t0) / steps * 1e3
+    live = None
+    if kernel_timing:
+        live = [s.elapsed_time(e) * 1e-3 for _, s, e in ops.kernel_timer]
+        ops.kernel_timer = None
+        ops.kernel_timer_only = None
 
     # forward-only throughput (no autograd graph)
     with torch.no_grad():
@@ -201,7 +253,7 @@ def gpu_run(cfg, steps, warmup, kernel_timing):
         torch.cuda.synchronize()
         f1 = time.perf_counter()
     ms_fwd = (f1 - f0) / steps * 1e3
-    return ms_step, ms_fwd, per, extra
+    return ms_step, ms_fwd, per, extra, (dominant, live)
 
 
 def copy_calib(mib: float):
@@ -267,6 +319,101 @@ def cpu_run(cfg, budget_s: float):
                       f"median of 3 after 1 warm-up, torch.set_num_threads({cores})"}
 
 
+# rocprofv3 kernel names of the launch groups bench.py times
+KERNEL_NAMES = {
+    "agg_fwd": ["agg_fwd_chunk", "agg_fwd_finalize"],
+    "agg_bwd": ["agg_bwd_chunk", "coeff_grad_finalize", "agg_frame_weights"],
+    "gate_fwd": ["gate_fwd_kernel"],
+    "gate_bwd": ["gate_bwd_kernel", "gate_bwd_finalize"],
+}
+
+
+def _pmc_per_kernel(db: str, counter: str):
+    """kernel name -> (dispatches, mean counter value per dispatch) from a rocprofv3 database."""
+    import sqlite3
+    c = sqlite3.connect(db)
+    rows = c.execute("select kernel_name, dispatch_id, sum(value) from counters_collection "
+                     "where counter_name = ? group by dispatch_id", (counter,)).fetchall()
+    agg = {}
+    for name, _, v in rows:
+        n, t = agg.get(name, (0, 0.0))
+        agg[name] = (n + 1, t + v)
+    return {k: (n, t / n) for k, (n, t) in agg.items()}
+
+
+COPY_CALIB_MIB = 144   # pmc_summary expects the calibration run made with --copy-calib 144
+
+
+def _gemm_groups(db: str):
+    """Library kernel name of each projection GEMM, from the dispatch order of
+    one layer step: qc_fwd precedes agg_fwd_chunk, ag_fwd follows gate_fwd,
+    ag_dgrad and ag_wgrad precede gate_bwd, qc_dgrad and qc_wgrad follow
+    coeff_grad_finalize."""
+    import sqlite3
+    c = sqlite3.connect(db)
+    seq = [r[0] for r in c.execute("select kernel_name from counters_collection group by dispatch_id "
+                                   "order by dispatch_id")]
+    order = ["gemm_qc_fwd", "gemm_ag_fwd", "gemm_ag_dgrad", "gemm_ag_wgrad", "gemm_qc_dgrad", "gemm_qc_wgrad"]
+    names = {}
+    # walk the last complete fwd+bwd step: from the last gate_bwd back to the agg_fwd before it
+    gb = max(i for i, n in enumerate(seq) if "gate_bwd_kernel" in n)
+    af = max(i for i, n in enumerate(seq[:gb]) if "agg_fwd_chunk" in n)
+    gemms = [n for n in seq[af - 3:] if "Cijk" in n][:6]
+    pre = [n for n in seq[:af] if "Cijk" in n]
+    if pre:
+        gemms = [pre[-1]] + [n for n in seq[af:] if "Cijk" in n][:5]
+    for g, n in zip(order, gemms):
+        names[g] = n[:160]
+    return names
+
+
+def pmc_summary(cfg_name, dbs):
+    """Calibrated HBM bytes per launch group: FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch) of each kernel, scaled by what the same counters read for a
+    plain device copy of known size (rocclr's copyBuffer blit)."""
+    fetch, write, cfetch, cwrite = (_pmc_per_kernel(d, c) for d, c in
+                                    zip(dbs, ["FETCH_SIZE", "WRITE_SIZE", "FETCH_SIZE", "WRITE_SIZE"]))
+    copy_bytes = COPY_CALIB_MIB * float(1 << 20)
+    ckf = max(((k, v) for k, v in cfetch.items() if "copyBuffer" in k), key=lambda kv: kv[1][1])
+    ckw = max(((k, v) for k, v in cwrite.items() if "copyBuffer" in k), key=lambda kv: kv[1][1])
+    f_scale = copy_bytes / (ckf[1][1] * 1024.0)
+    w_scale = copy_bytes / (ckw[1][1] * 1024.0)
+    out = {"config": cfg_name, "copy_calib_bytes_each_way": copy_bytes, "fetch_scale": f_scale,
+           "write_scale": w_scale, "kernels": {}}
+    for name in fetch:
+        fb = fetch[name][1] * 1024.0 * f_scale
+        wb = write.get(name, (0, 0.0))[1] * 1024.0 * w_scale
+        out["kernels"][name[:160]] = {"fetch_bytes": fb, "write_bytes": wb, "dispatches": fetch[name][0]}
+    groups = {}
+    for g, names in KERNEL_NAMES.items():
+        tot = 0.0
+        for kname, v in out["kernels"].items():
+            if any(n in kname for n in names):
+                tot += v["fetch_bytes"] + v["write_bytes"]
+        groups[g] = tot
+    gg = _gemm_groups(dbs[0])
+    for g, kname in gg.items():
+        v = out["kernels"].get(kname)
+        if v is not None:
+            groups[g] = v["fetch_bytes"] + v["write_bytes"]
+    out["gemm_kernels"] = gg
+    out["groups"] = groups
+    path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps({"wrote": path, "groups": groups, "fetch_scale": f_scale, "write_scale": w_scale}))
+
+
+def traffic_of(cfg_name, group):
+    """HBM bytes per launch of a launch group from profiles/traffic_<config>.json, or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("groups", {}).get(group)
+    except (OSError, ValueError):
+        return None
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -276,8 +423,12 @@ def main():
     if a.copy_calib > 0:
         copy_calib(a.copy_calib)
         return
+    if a.pmc_summary:
+        pmc_summary(a.config, a.pmc_summary)
+        return
     cfg = CONFIGS[a.config]
-    ms_step, ms_fwd, per, extra = gpu_run(cfg, a.steps, a.warmup, not a.no_kernel_timing)
+    ms_step, ms_fwd, per, extra, (dominant, live) = gpu_run(cfg, a.steps, a.warmup,
+                                                            not a.no_kernel_timing and not a.graph, a.graph)
     T = cfg["B"] * cfg["N"]
     work = kernel_work(cfg, extra)
     kernels = {}
@@ -292,12 +443,17 @@ def main():
                          "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4),
                          "launches_per_step": len(durs) / a.steps}
     roofline = None
-    if kernels:
-        dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
-        k = kernels[dom]
-        roofline = {"kernel": dom, "bound": k["bound"], "achieved": k["achieved"],
-                    "peak": 8000.0 if k["bound"] == "hbm" else 2500.0, "unit": k["unit"], "frac": k["frac"],
-                    "traffic": None}
+    if kernels and dominant and live:
+        k = kernels[dominant]
+        bound, amount = work[dominant]
+        avg = sum(live) / len(live)                      # from the timed region's events
+        achieved = amount / avg
+        peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
+        roofline = {"kernel": dominant, "bound": bound,
+                    "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
+                    "peak": 8000.0 if bound == "hbm" else 2500.0, "unit": k["unit"],
+                    "frac": round(achieved / peak, 4), "avg_us": round(avg * 1e6, 2),
+                    "launches_timed": len(live), "traffic": traffic_of(a.config, dominant)}
     res = {
         "metric": METRIC, "value": round(T / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
@@ -305,7 +461,8 @@ def main():
         "data": "synthetic: x~N(0,1) seed 1, upstream grad~N(0,1) seed 2, weights nn.Linear init seed 0",
         "config": {"workload": cfg["workload"], "B": cfg["B"], "N": cfg["N"], "D": cfg["D"], "degree": cfg["K"],
                    "expand": cfg["E"], "tokens_per_step": T},
-        "fwd_tokens_per_s": round(T / (ms_fwd * 1e-3), 1), "ms_fwd": round(ms_fwd, 4),
+        "fwd_tokens_per_s": round(T / (ms_fwd * 1e-3), 1) if ms_fwd else None,
+        "ms_fwd": round(ms_fwd, 4) if ms_fwd else None, "hip_graph": a.graph,
         "roofline": roofline, "kernels": kernels,
     }
     if kernels:

@@ -48,16 +48,19 @@ int ilog2_ceil(int64_t v) {
 // shortest chunk worth its own workgroup.
 struct Tune {
   int lpr_log2 = 3;        // 8 lanes x 16 bytes = 128-byte row segments
-  int64_t target_wg = 1024;
+  int64_t target_wg = 1024;      // gating kernels
+  int64_t agg_target_wg = 512;   // aggregation: one chunk per row when B * slabs reaches it
   int64_t min_rows = 128;
   int64_t scan_target_wg = 2048;
   Tune() {
     if (const char* s = getenv("POM_AMD_LPR_LOG2")) lpr_log2 = atoi(s);
     if (const char* s = getenv("POM_AMD_TARGET_WG")) target_wg = atoll(s);
+    if (const char* s = getenv("POM_AMD_AGG_TARGET_WG")) agg_target_wg = atoll(s);
     if (const char* s = getenv("POM_AMD_MIN_ROWS")) min_rows = atoll(s);
     if (const char* s = getenv("POM_AMD_SCAN_TARGET_WG")) scan_target_wg = atoll(s);
     if (lpr_log2 < 0 || lpr_log2 > 4) lpr_log2 = 3;
     if (target_wg < 1) target_wg = 1024;
+    if (agg_target_wg < 1) agg_target_wg = 512;
     if (min_rows < 1) min_rows = 128;
     if (scan_target_wg < 1) scan_target_wg = 2048;
   }
@@ -101,9 +104,9 @@ void choose_slabs(pom::Geom& g) {
 // frame's grid reaches the target or chunks would drop below min_rows.  The
 // choice ignores the frame count on purpose: a frame is then summed in the
 // same order whether it arrives alone (PoM.state_forward) or among others.
-void choose_chunks(pom::Geom& g, int64_t B) {
+void choose_chunks(pom::Geom& g, int64_t B, int64_t target) {
   int64_t cpf = 1;
-  while (B * cpf * g.nslabs < tune().target_wg && cdiv(g.L, 2 * cpf) >= tune().min_rows) cpf *= 2;
+  while (B * cpf * g.nslabs < target && cdiv(g.L, 2 * cpf) >= tune().min_rows) cpf *= 2;
   g.RC = cdiv(g.L, cpf);
   g.cpf = cdiv(g.L, g.RC);
   g.nch = g.F * g.cpf;
@@ -237,7 +240,7 @@ int setup_agg(pom::AggParams& p, int dtype, int64_t B, int64_t N, int64_t P, int
     p.g.L = frame_len;
     p.g.F = N / frame_len;
   }
-  choose_chunks(p.g, B);
+  choose_chunks(p.g, B, tune().agg_target_wg);
   if (p.g.nslabs > 0x7fffffffLL || p.g.nch > 65535 || B > 65535)
     return fail(POM_ERR_UNSUPPORTED, "grid too large (slabs %lld, chunks %lld, B %lld)", (long long)p.g.nslabs,
                 (long long)p.g.nch, (long long)B);
@@ -311,7 +314,7 @@ int setup_gate(pom::GateParams& p, int& per_token, int dtype, int64_t B, int64_t
     p.g.F = groups;
     p.g.L = N / groups;
   }
-  choose_chunks(p.g, B);
+  choose_chunks(p.g, B, tune().target_wg);
   if (p.g.nch > 65535 || B > 65535) return fail(POM_ERR_UNSUPPORTED, "grid too large");
   return POM_OK;
 }

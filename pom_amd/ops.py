@@ -19,6 +19,7 @@ and its backward writes grad_x straight into the matching half of dY.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Optional, Tuple
 
 import torch
@@ -32,6 +33,7 @@ from .gemm_select import tuned_gemms
 # site below appends (name, start_event, end_event) recorded on the stream the
 # launch goes to.  bench.py uses it to time each kernel inside its timed region.
 kernel_timer: Optional[list] = None
+kernel_timer_only: Optional[set] = None   # record only these names (None: all)
 
 
 class _Span:
@@ -42,7 +44,7 @@ class _Span:
         self.ev = None
 
     def __enter__(self):
-        if kernel_timer is not None:
+        if kernel_timer is not None and (kernel_timer_only is None or self.name in kernel_timer_only):
             self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             self.ev[0].record()
         return self
@@ -61,10 +63,36 @@ def _check_degree(k: int) -> None:
         raise ValueError(f"degree must be >= 1 (got {k})")
 
 
+_f32_cache: dict = {}
+
+
+def _as_f32(t: torch.Tensor) -> torch.Tensor:
+    """fp32 contiguous copy of a small parameter (coefficients, gate bias), kept
+    while that same tensor object is alive and unchanged (identity, storage
+    pointer and version counter), so a bf16 model does not pay a conversion
+    kernel per call.  Keyed by object identity: a freed tensor's address or id
+    reused by a new tensor can never hit a stale copy."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.detach()
+    hit = _f32_cache.get(id(t))
+    if hit is not None:
+        ref, version, ptr, c = hit
+        if ref() is t and version == t._version and ptr == t.data_ptr():
+            return c
+    c = t.detach().float().contiguous()
+    if len(_f32_cache) > 64:
+        for k in [k for k, v in _f32_cache.items() if v[0]() is None]:
+            del _f32_cache[k]
+        if len(_f32_cache) > 64:
+            _f32_cache.clear()
+    _f32_cache[id(t)] = (weakref.ref(t), t._version, t.data_ptr(), c)
+    return c
+
+
 def _coeff32(coeff: torch.Tensor, p: int, k: int) -> torch.Tensor:
     if coeff.shape != (p, k):
         raise ValueError(f"coeff must have shape ({p}, {k}), got {tuple(coeff.shape)}")
-    return coeff.detach().float().contiguous()
+    return _as_f32(coeff)
 
 
 # ---------------------------------------------------------------------------
@@ -329,7 +357,7 @@ class _PoMLayer(torch.autograd.Function):
         h_view, s_view = y3[..., :P], y3[..., P:]
         c32 = _coeff32(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
-        b32 = se_bias.detach().float().contiguous()
+        b32 = _as_f32(se_bias)
         sh = gate_forward(s_view, b32, hagg, rope_s)                # (B, N, P)
         wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
         with _Span("gemm_ag_fwd"), tuned_gemms():
@@ -337,6 +365,7 @@ class _PoMLayer(torch.autograd.Function):
         if b_ag is not None:
             out = out + b_ag.to(dt)
         ctx.save_for_backward(x, y, sh, hagg, c32, b32, wq, wa, mask, count)
+        ctx.set_materialize_grads(False)   # the aggregate output is usually unused
         ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None)
         ctx.dtypes = (w_qc.dtype, se_bias.dtype, coeff.dtype, w_ag.dtype,
                       None if b_ag is None else b_ag.dtype)
@@ -347,6 +376,8 @@ class _PoMLayer(torch.autograd.Function):
         x, y, sh, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
         k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias = ctx.meta
         B, N, D = x.shape
+        if grad_out is None:   # only the aggregate was used downstream
+            grad_out = torch.zeros(B, N, D, dtype=x.dtype, device=x.device)
         P = c32.shape[0]
         T = B * N
         dt = x.dtype
