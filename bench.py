@@ -151,6 +151,12 @@ def kernel_work(cfg, extra):
         "gate_fwd": ("hbm", float(2 * T * P * e + B * G * P * 4)),
         # y_s and dsh read, dy_s written
         "gate_bwd": ("hbm", float(3 * T * P * e + B * G * P * 4)),
+        # operand-layout transposes for the backward GEMMs: read + write once
+        "transpose_x": ("hbm", float(2 * T * D * e)),
+        "transpose_sh": ("hbm", float(2 * T * P * e)),
+        "transpose_g": ("hbm", float(2 * T * D * e)),
+        "transpose_dy": ("hbm", float(2 * T * 2 * P * e)),
+        "transpose_w": ("hbm", float(2 * 2 * P * D * e)),   # W_qc or W_ag: counted as the larger
     }
     return w
 
@@ -176,6 +182,9 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
         for p in params:
             p.grad = None
         xd.grad = None
+        # a training step changes every parameter: rebuild the per-parameter
+        # derived copies (fp32 coefficients, transposed weights) every step
+        ops.invalidate_derived()
         out = fwd(m, xd)
         out.backward(god)
 

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 2
+#define POM_AMD_ABI_VERSION 3
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -53,6 +53,19 @@ typedef struct pom_view {
   int64_t stride_b;
   int64_t stride_n;
 } pom_view;
+
+/* Optional channel-major ("transposed") copy of a (B, N, C) output: element
+ * (b, n, c) at data[c * stride_c + b * stride_b + n], in elements.  The
+ * backward's weight-gradient GEMMs reduce over tokens and take operands that
+ * are contiguous along them; the kernels that produce sh and dY write this
+ * copy in the same pass.  Built for 16-bit types with 16-byte lanes (every
+ * channel count a multiple of 8 and 16-byte-aligned views); other requests
+ * return POM_ERR_UNSUPPORTED before anything is launched.  NULL: none. */
+typedef struct pom_tview {
+  void* data;
+  int64_t stride_c;
+  int64_t stride_b;
+} pom_tview;
 
 /* Rotary tables (fp32) and integer token positions.
  *   1-D: cos0/sin0 (rows0, P/2), pos[n * pos_stride]           (pom/pom_rope.py:93-117, :152-180)
@@ -118,6 +131,7 @@ int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
 /* Backward.  grad_out: (B, N/frame_len, P) fp32.  count: (B,) fp32 from the
  * forward (masked mode).  grad_x: view written for every token (0 where the
  * mask is 0); may alias a slice of a larger buffer (e.g. the h-half of dY).
+ * grad_x_t: channel-major copy of grad_x, or NULL (not in token-causal mode).
  * grad_coeff: (P, K) fp32, overwritten.  The gradient of `carry` is
  * n_past * sum_f grad_out[f] / (n_past + f + 1) and is left to the caller. */
 int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
@@ -126,7 +140,8 @@ int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
                 const float* count,
                 int64_t frame_len, int64_t n_past,
                 const pom_rope* rope,
-                const float* grad_out, const pom_view* grad_x, float* grad_coeff,
+                const float* grad_out, const pom_view* grad_x, const pom_tview* grad_x_t,
+                float* grad_coeff,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
@@ -138,17 +153,34 @@ int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
 size_t pom_gate_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t groups,
                                int rope_kind);
 
+/* sh_t: channel-major copy of sh, or NULL. */
 int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P,
                  const pom_view* ys, const float* bias, const void* hagg, int64_t groups,
-                 const pom_rope* rope, const pom_view* sh, void* stream);
+                 const pom_rope* rope, const pom_view* sh, const pom_tview* sh_t, void* stream);
 
-/* Backward.  grad_ys: view (e.g. the s-half of dY) receiving dL/dy_s.
+/* Backward.  grad_ys: view (e.g. the s-half of dY) receiving dL/dy_s;
+ * grad_ys_t: its channel-major copy, or NULL.
  * grad_hagg: (B, groups, P) fp32, 16-byte aligned.  grad_bias: (P,) fp32 or NULL. */
 int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P,
                  const pom_view* ys, const float* bias, const void* hagg, int64_t groups,
                  const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
-                 float* grad_hagg, float* grad_bias,
+                 const pom_tview* grad_ys_t, float* grad_hagg, float* grad_bias,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Operand layout
+ * ------------------------------------------------------------------------ */
+
+/* dst (cols x rows, row stride ld_dst) = src^T (rows x cols, row stride
+ * ld_src), in elements of dtype.  Out of place, on `stream`.
+ * No counterpart in the reference (which leaves operand layout to its GEMM
+ * library): the fused layer uses it to give its projection GEMMs operands
+ * that are contiguous along the reduction dimension (token-contiguous x^T,
+ * g^T, sh^T, dY^T for the weight gradients; transposed weights for the data
+ * gradients).  16-byte-aligned operands with strides a multiple of 16 bytes
+ * take the vector path. */
+int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src,
+                  void* dst, int64_t ld_dst, void* stream);
 
 #ifdef __cplusplus
 }

@@ -26,7 +26,7 @@ POM_ERR_DEVICE = 4
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
 MAX_DEGREE = 16
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # Every symbol include/pom_amd.h declares, with its ctypes signature.
 _c_i64 = ctypes.c_int64
@@ -45,8 +45,13 @@ class PomRope(ctypes.Structure):
                 ("pos_stride", _c_i64)]
 
 
+class PomTView(ctypes.Structure):
+    _fields_ = [("data", _c_vp), ("stride_c", _c_i64), ("stride_b", _c_i64)]
+
+
 _PV = ctypes.POINTER(PomView)
 _PR = ctypes.POINTER(PomRope)
+_PT = ctypes.POINTER(PomTView)
 
 SIGNATURES = {
     "pom_abi_version": (_c_int, []),
@@ -55,11 +60,12 @@ SIGNATURES = {
     "pom_agg_fwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64, _c_i64,
                              _c_i64, _c_vp, _c_i64, _PR, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "pom_agg_bwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64, _c_i64,
-                             _c_vp, _c_i64, _c_i64, _PR, _c_vp, _PV, _c_vp, _c_vp, _c_size, _c_vp]),
+                             _c_vp, _c_i64, _c_i64, _PR, _c_vp, _PV, _PT, _c_vp, _c_vp, _c_size, _c_vp]),
     "pom_gate_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),
-    "pom_gate_fwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR, _PV, _c_vp]),
-    "pom_gate_bwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR, _PV, _PV,
+    "pom_gate_fwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR, _PV, _PT, _c_vp]),
+    "pom_gate_bwd": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR, _PV, _PV, _PT,
                               _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "pom_transpose": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -121,6 +127,17 @@ def require_device(*tensors: torch.Tensor) -> None:
         if t is not None and not t.is_cuda:
             raise RuntimeError("pom_amd runs on ROCm devices only (got a CPU tensor); "
                                "move the module and inputs to a GPU")
+
+
+def tview(t: Optional["torch.Tensor"], B: int, N: int):
+    """Channel-major copy target: a (C, B*N) tensor with unit token stride, as
+    a PomTView (element (b, n, c) at c * stride_c + b * N + n), or None."""
+    if t is None:
+        return None
+    if t.dim() != 2 or t.shape[1] != B * N or t.stride(1) != 1:
+        raise ValueError(f"channel-major copy must be (C, {B * N}) with unit token stride, got "
+                         f"{tuple(t.shape)} strides {t.stride()}")
+    return ctypes.byref(PomTView(t.data_ptr(), t.stride(0), N))
 
 
 def view3(t: torch.Tensor) -> PomView:

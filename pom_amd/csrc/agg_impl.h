@@ -70,11 +70,21 @@ struct Mode_ {
 // is full; the last clamps its row indices into the chunk (so every load
 // stays in bounds and is issued without a branch) and its compute drops the
 // rows past the end.
+//
+// RowWalk::consecutive gives each lane U adjacent rows instead
+// (row base + row0 * U + u): the kernels that also write a channel-major copy
+// of their output use it, so a lane holds U consecutive tokens of each of its
+// channels, one vector write per channel into the staging tile.
 struct RowWalk {
   int64_t rbeg, nrows, step;
   int row0, rs;
   __device__ __forceinline__ RowWalk(int64_t rbeg_, int64_t rend_, int row0_, int rs_, int U)
       : rbeg(rbeg_), nrows(rend_ - rbeg_), step((int64_t)rs_ * U), row0(row0_), rs(rs_) {}
+  __device__ __forceinline__ static RowWalk consecutive(int64_t rbeg_, int64_t rend_, int row0_, int rs_, int U) {
+    RowWalk w(rbeg_, rend_, row0_ * U, 1, U);
+    w.step = (int64_t)rs_ * U;
+    return w;
+  }
   __device__ __forceinline__ int64_t full_steps() const { return nrows / step; }
   __device__ __forceinline__ bool has_tail() const { return full_steps() * step < nrows; }
   __device__ __forceinline__ bool valid(int64_t base, int u) const { return base + row0 + (int64_t)u * rs < nrows; }
@@ -85,6 +95,96 @@ struct RowWalk {
     return rbeg + rel;
   }
 };
+
+// Walk over a chunk's steps: load(buf, base, clamp) fills buf with the rows
+// of the step at `base` (clamped into the chunk for the tail step), then
+// work(buf, base, tail_tag) consumes them.  The step count is the same for
+// every lane of the workgroup, so work() may synchronise the workgroup.
+template <typename Buf, typename Load, typename Work>
+__device__ __forceinline__ void walk_rows(const RowWalk& W, Load&& load, Work&& work) {
+  const int64_t nfull = W.full_steps();
+  for (int64_t it = 0; it < nfull; ++it) {
+    Buf bf;
+    load(bf, it * W.step, false);
+    work(bf, it * W.step, std::false_type{});
+  }
+  if (W.has_tail()) {
+    Buf bf;
+    load(bf, nfull * W.step, true);
+    work(bf, nfull * W.step, std::true_type{});
+  }
+}
+
+// Channel-major copy of one workgroup step, staged through LDS.  The step
+// covers tokens [tok0, tok0 + S) of batch row b, S = kWaves * rpw * U, for
+// the lpr * NS channel slots of the slab; each lane holds U consecutive tokens
+// of its NS slots (RowWalk::consecutive).  Lanes write their U x NS block into
+// an LDS tile (one row per slot), then the workgroup stores the tile row by
+// row: a store instruction writes runs of S tokens of one channel (512 bytes
+// for bf16 at U = 8) where direct stores from the lanes would write 128-byte
+// pieces of eight channel rows each, which measured 2-3x slower.
+// chan(l, i): channel of slot i of lane column l, or -1 past the channels.
+// nvalid: tokens of the step inside the chunk.  Every wave of the workgroup
+// calls it once per step (it synchronises the workgroup).
+// Channel of slot i of lane column l of a slab (LaneMap), or -1 past the channels.
+template <int CPT, int MODE>
+__device__ __forceinline__ int64_t slab_chan(int64_t slab, int lpr, int64_t nvec, int64_t P, int l, int i) {
+  const int64_t vc = slab * lpr + l;
+  if (vc >= nvec) return -1;
+  LaneMap<CPT, MODE> m;
+  m.init(vc, P);
+  return m.chan(i);
+}
+
+template <int U, int NS>
+struct TrTile {
+  static constexpr int kElems = kWaves * kWave * U * NS + 8 * kMaxLpr * NS;
+};
+
+template <typename T, int U, int NS, typename Chan>
+__device__ __forceinline__ void store_tr_staged(const TrOut& t, const LaneGeom& G, int64_t b, int64_t tok0,
+                                                int64_t nvalid, const Chan& chan, const float (&v)[U][NS],
+                                                T* tile) {
+  const int S = kWaves * G.rpw * U;          // tokens per step
+  const int pitch = S + 8;                   // elements; rows start on distinct banks
+  const int R = G.lpr * NS;                  // channel slots of the slab
+  __syncthreads();                           // the previous step's readers are done
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    float col[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) col[u] = v[u][i];
+    VecIO<T, U>::store(tile + (G.lcol * NS + i) * pitch + (G.wave * G.rpw + G.lrow) * U, col);
+  }
+  __syncthreads();
+  using Raw = typename RawVec<16>::type;
+  T* base = reinterpret_cast<T*>(t.data) + b * t.sb + tok0;
+  const bool vec = t.ld % 8 == 0 && reinterpret_cast<uintptr_t>(base) % 16 == 0;
+  const int CR = S / 8;                      // 16-byte chunks per tile row
+  for (int idx = G.tid; idx < R * CR; idx += kThreads) {
+    const int row = idx / CR, c = idx - row * CR;
+    const int64_t ch = chan(row / NS, row % NS);
+    const int tok = c * 8;
+    if (ch < 0 || tok >= nvalid) continue;
+    const T* src = tile + row * pitch + tok;
+    T* dst = base + ch * t.ld + tok;
+    if (vec && tok + 8 <= nvalid) {
+      *reinterpret_cast<Raw*>(dst) = *reinterpret_cast<const Raw*>(src);
+    } else {
+      for (int e = 0; e < 8 && tok + e < nvalid; ++e) dst[e] = src[e];
+    }
+  }
+}
+
+// Zeros in the channel-major copy for tokens [n_lo, n_hi) of batch row b and
+// the nch channels starting at c0 (rows a masked kernel never loads).
+template <typename T>
+__device__ __forceinline__ void zero_tr(const TrOut& t, int64_t b, int64_t n_lo, int64_t n_hi,
+                                        int64_t c0, int64_t nch) {
+  T* base = reinterpret_cast<T*>(t.data) + b * t.sb;
+  for (int64_t c = 0; c < nch; ++c)
+    for (int64_t n = n_lo + threadIdx.x; n < n_hi; n += kThreads) base[(c0 + c) * t.ld + n] = from_f32<T>(0.0f);
+}
 
 // Masked mode: the chunk's first and last rows with a nonzero weight and the
 // sum of its weights, from one pass over the chunk's mask entries.  Rows
@@ -137,7 +237,7 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
   constexpr bool ROPE = Mode_<MODE>::rope;
   constexpr bool MASKED = MODE == MODE_MASKED;
   constexpr int U = Mode_<MODE>::U;
-  __shared__ float red[kWaves][16 * CPT2];
+  __shared__ float red[kWaves][kMaxLpr * CPT2];
 
   const LaneGeom G(p.g.lpr_log2);
   const int64_t slab = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
@@ -168,18 +268,25 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
   const T* xb = reinterpret_cast<const T*>(p.x) + b * p.sxb;
   const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
 
-  auto step = [&](int64_t base, auto tail_tag) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
+  struct Buf {
     Pack<T, CPT> v1[U], v2[ROPE ? U : 1];
     float wv[U];
+  };
+  auto load = [&](Buf& bf, int64_t base, bool clamp) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t rr = W.row(base, u, TAIL);
+      const int64_t rr = W.row(base, u, clamp);
       const T* row = xb + rr * p.sxn;
-      v1[u].load(row + map.c1);
-      if constexpr (ROPE) v2[u].load(row + map.c2);
-      if constexpr (MASKED) wv[u] = p.mask[b * p.msb + rr * p.msn];
+      bf.v1[u].load(row + map.c1);
+      if constexpr (ROPE) bf.v2[u].load(row + map.c2);
+      if constexpr (MASKED) bf.wv[u] = p.mask[b * p.msb + rr * p.msn];
     }
+  };
+  auto step = [&](const Buf& bf, int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    const auto& v1 = bf.v1;
+    const auto& v2 = bf.v2;
+    const auto& wv = bf.wv;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       bool keep = !TAIL || W.valid(base, u);
@@ -212,11 +319,7 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
     }
   };
 
-  if (active) {
-    const int64_t nfull = W.full_steps();
-    for (int64_t it = 0; it < nfull; ++it) step(it * W.step, std::false_type{});
-    if (W.has_tail()) step(nfull * W.step, std::true_type{});
-  }
+  if (active) walk_rows<Buf>(W, load, step);
 
   // Rows -> one value per column: shuffles inside the wave, LDS across waves.
 #pragma unroll
@@ -316,14 +419,14 @@ static __global__ void __launch_bounds__(kThreads) agg_frame_weights(const AggPa
 // Backward chunk kernel: grad_x for every row of the chunk (written into a
 // strided view, e.g. the h-half of dY) and the chunk's grad_coeff partial.
 // ---------------------------------------------------------------------------
-template <typename T, int CPT, int KM, int MODE>
+template <typename T, int CPT, int KM, int MODE, bool TR>
 __global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
   constexpr bool MASKED = MODE == MODE_MASKED;
   constexpr int U = Mode_<MODE>::U;
-  __shared__ float red[kWaves][16 * CPT2];
+  __shared__ float red[kWaves][kMaxLpr * CPT2];
 
   const LaneGeom G(p.g.lpr_log2);
   const int64_t slab = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
@@ -381,23 +484,40 @@ __global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
       for (int64_t n = last + G.wave * G.rpw + G.lrow; n < rend; n += G.rs)
         VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
     }
+    if constexpr (TR) {
+      const int64_t c0 = slab * G.lpr * CPT;
+      const int64_t nc = p.P - c0 < G.lpr * CPT ? p.P - c0 : G.lpr * CPT;
+      zero_tr<T>(p.gxt, b, rbeg, first, c0, nc);
+      zero_tr<T>(p.gxt, b, last, rend, c0, nc);
+    }
     rbeg = first;
     rend = last;
   }
-  const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+  const RowWalk W = TR ? RowWalk::consecutive(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U)
+                       : RowWalk(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+  __shared__ __attribute__((aligned(16))) unsigned char tile_raw[TR ? TrTile<U, CPT2>::kElems * sizeof(T) : 16];
+  T* tile = reinterpret_cast<T*>(tile_raw);
 
-  auto step = [&](int64_t base, auto tail_tag) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
+  struct Buf {
     Pack<T, CPT> v1[U], v2[ROPE ? U : 1];
     float mv[U];
+  };
+  auto load = [&](Buf& bf, int64_t base, bool clamp) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t rr = W.row(base, u, TAIL);
+      const int64_t rr = W.row(base, u, clamp);
       const T* row = xb + rr * p.sxn;
-      v1[u].load(row + map.c1);
-      if constexpr (ROPE) v2[u].load(row + map.c2);
-      if constexpr (MASKED) mv[u] = p.mask[b * p.msb + rr * p.msn];
+      bf.v1[u].load(row + map.c1);
+      if constexpr (ROPE) bf.v2[u].load(row + map.c2);
+      if constexpr (MASKED) bf.mv[u] = p.mask[b * p.msb + rr * p.msn];
     }
+  };
+  auto step = [&](const Buf& bf, int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    float gt[TR ? U : 1][CPT2];
+    const auto& v1 = bf.v1;
+    const auto& v2 = bf.v2;
+    const auto& mv = bf.mv;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool in = !TAIL || W.valid(base, u);
@@ -419,9 +539,16 @@ __global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
           pow_acc<KM>(in ? h1 : 0.0f, wa, g[i]);
           pow_acc<KM>(in ? h2 : 0.0f, wb, g[CPT + i]);
         }
-        if (in) {
+        if (active && in) {
           VecIO<T, CPT>::store(grow + map.c1, gv1);
           VecIO<T, CPT>::store(grow + map.c2, gv2);
+        }
+        if constexpr (TR) {
+#pragma unroll
+          for (int i = 0; i < CPT; ++i) {
+            gt[u][i] = gv1[i];
+            gt[u][CPT + i] = gv2[i];
+          }
         }
       } else {
         bool keep = in;
@@ -440,16 +567,24 @@ __global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
             pow_sum<KM>(TAIL ? (in ? h : 0.0f) : h, g[i]);   // scaled by w at the end
           }
         }
-        if (in) VecIO<T, CPT>::store(grow + map.c1, gv1);
+        if (active && in) VecIO<T, CPT>::store(grow + map.c1, gv1);
+        if constexpr (TR) {
+#pragma unroll
+          for (int i = 0; i < CPT; ++i) gt[u][i] = gv1[i];
+        }
       }
+    }
+    if constexpr (TR) {
+      const int64_t left = W.nrows - base;
+      store_tr_staged<T, U, CPT2>(
+          p.gxt, G, b, W.rbeg + base, left < W.step ? left : W.step,
+          [&](int l, int i) { return slab_chan<CPT, MODE>(slab, G.lpr, p.g.nvec, p.P, l, i); }, gt, tile);
     }
   };
 
-  if (active) {
-    const int64_t nfull = W.full_steps();
-    for (int64_t it = 0; it < nfull; ++it) step(it * W.step, std::false_type{});
-    if (W.has_tail()) step(nfull * W.step, std::true_type{});
-  }
+  // every lane walks (lanes past the channels on channel 0 with zero weights,
+  // storing nothing): the staged channel-major stores synchronise the workgroup
+  walk_rows<Buf>(W, load, step);
   if constexpr (!ROPE && !MASKED) {
 #pragma unroll
     for (int i = 0; i < CPT2; ++i)
@@ -523,17 +658,32 @@ hipError_t agg_fwd_mode(const AggParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <typename T, int CPT, int KM>
-hipError_t agg_bwd_mode(const AggParams& p, hipStream_t st) {
+template <typename T, int CPT, int KM, bool TR>
+hipError_t agg_bwd_tr(const AggParams& p, hipStream_t st) {
   const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
   switch (p.mode) {
-    case MODE_PLAIN: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_PLAIN>), grid, block, 0, st, p); break;
-    case MODE_MASKED: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_MASKED>), grid, block, 0, st, p); break;
-    case MODE_ROPE1D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D>), grid, block, 0, st, p); break;
-    case MODE_ROPE2D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D>), grid, block, 0, st, p); break;
+    case MODE_PLAIN: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_PLAIN, TR>), grid, block, 0, st, p); break;
+    case MODE_MASKED: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_MASKED, TR>), grid, block, 0, st, p); break;
+    case MODE_ROPE1D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D, TR>), grid, block, 0, st, p); break;
+    case MODE_ROPE2D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D, TR>), grid, block, 0, st, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// The channel-major copy is built for 16-bit types with 16-byte lanes only
+// (the C ABI rejects other requests).
+template <typename T, int CPT>
+constexpr bool kTrBuilt = sizeof(T) == 2 && CPT == 8;
+
+template <typename T, int CPT, int KM>
+hipError_t agg_bwd_mode(const AggParams& p, hipStream_t st) {
+  if constexpr (kTrBuilt<T, CPT>) {
+    if (p.gxt.data) return agg_bwd_tr<T, CPT, KM, true>(p, st);
+  } else {
+    if (p.gxt.data) return hipErrorInvalidValue;
+  }
+  return agg_bwd_tr<T, CPT, KM, false>(p, st);
 }
 
 // Degree bound KM: exact for K <= 4, then 8 and 16 with zero coefficients.

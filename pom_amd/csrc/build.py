@@ -15,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "capi.cpp"]
+SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "transpose.hip", "capi.cpp"]
 OUT = os.path.join(PKG, "libpom_amd.so")
 BUILD_DIR = os.path.join(PKG, "_build")
 

@@ -58,7 +58,7 @@ struct Tune {
     if (const char* s = getenv("POM_AMD_AGG_TARGET_WG")) agg_target_wg = atoll(s);
     if (const char* s = getenv("POM_AMD_MIN_ROWS")) min_rows = atoll(s);
     if (const char* s = getenv("POM_AMD_SCAN_TARGET_WG")) scan_target_wg = atoll(s);
-    if (lpr_log2 < 0 || lpr_log2 > 4) lpr_log2 = 3;
+    if (lpr_log2 < 0 || lpr_log2 > 6) lpr_log2 = 3;
     if (target_wg < 1) target_wg = 1024;
     if (agg_target_wg < 1) agg_target_wg = 512;
     if (min_rows < 1) min_rows = 128;
@@ -268,6 +268,23 @@ size_t agg_ws_bytes(int64_t B, int64_t N, int64_t P, int K, int64_t frame_len, b
   return bwd ? carve_bytes({B * nc * K * P, B * F * P}) : carve_bytes({B * nc * P, B * nc});
 }
 
+// Channel-major copy requested by `tv` (or none): validated against the
+// geometry chosen for the launch.
+int set_tview(pom::TrOut& t, const pom_tview* tv, int dtype, int cpt, int64_t B, int64_t N, const char* name) {
+  if (!tv) return POM_OK;
+  if (!tv->data) return fail(POM_ERR_INVALID, "%s: data is null", name);
+  if (dtype == POM_DTYPE_F32 || cpt != 8)
+    return fail(POM_ERR_UNSUPPORTED, "%s: the channel-major copy needs 16-bit elements and 16-byte lanes", name);
+  if (!aligned(tv->data, 2)) return fail(POM_ERR_INVALID, "%s: data must be element-aligned", name);
+  if (tv->stride_b < N || tv->stride_c < (B - 1) * tv->stride_b + N)
+    return fail(POM_ERR_INVALID, "%s: strides (c %lld, b %lld) overlap for B=%lld N=%lld", name,
+                (long long)tv->stride_c, (long long)tv->stride_b, (long long)B, (long long)N);
+  t.data = tv->data;
+  t.ld = tv->stride_c;
+  t.sb = tv->stride_b;
+  return POM_OK;
+}
+
 int need_ws(void* ws, size_t have, size_t need) {
   if (!ws) return fail(POM_ERR_WORKSPACE, "workspace is null (need %zu bytes)", need);
   if (have < need) return fail(POM_ERR_WORKSPACE, "workspace %zu bytes, need %zu", have, need);
@@ -381,8 +398,8 @@ int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_vie
 int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x, const float* coeff,
                 const float* mask, int64_t mask_stride_b, int64_t mask_stride_n, const float* count,
                 int64_t frame_len, int64_t n_past, const pom_rope* rope, const float* grad_out,
-                const pom_view* grad_x, float* grad_coeff, void* workspace, size_t workspace_bytes,
-                void* stream) {
+                const pom_view* grad_x, const pom_tview* grad_x_t, float* grad_coeff, void* workspace,
+                size_t workspace_bytes, void* stream) {
   pom::AggParams p;
   if (int r = check_view(grad_x, "grad_x")) return r;
   if (int r = setup_agg(p, dtype, B, N, P, K, x, coeff, mask, mask_stride_b, mask_stride_n, frame_len, rope,
@@ -392,6 +409,9 @@ int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_vie
   if (mask && !count) return fail(POM_ERR_INVALID, "masked backward needs the forward's count");
   if (n_past < 0) return fail(POM_ERR_INVALID, "negative n_past");
   if (n_past > 0 && frame_len == 1 && N > 1) return fail(POM_ERR_UNSUPPORTED, "carry with token-causal aggregation");
+  if (grad_x_t && frame_len == 1 && N > 1)
+    return fail(POM_ERR_UNSUPPORTED, "grad_x_t with token-causal aggregation");
+  if (int r = set_tview(p.gxt, grad_x_t, dtype, p.g.cpt, B, N, "grad_x_t")) return r;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (int r = need_ws(workspace, workspace_bytes, agg_ws_bytes(B, N, P, K, frame_len, true))) return r;
   Carve c{static_cast<char*>(workspace), 0};
@@ -427,11 +447,13 @@ size_t pom_gate_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64
 }
 
 int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys, const float* bias,
-                 const void* hagg, int64_t groups, const pom_rope* rope, const pom_view* sh, void* stream) {
+                 const void* hagg, int64_t groups, const pom_rope* rope, const pom_view* sh, const pom_tview* sh_t,
+                 void* stream) {
   pom::GateParams p;
   int per_token = 0;
   if (int r = check_view(sh, "sh")) return r;
   if (int r = setup_gate(p, per_token, dtype, B, N, P, ys, hagg, groups, rope, {sh})) return r;
+  if (int r = set_tview(p.sht, sh_t, dtype, p.g.cpt, B, N, "sh_t")) return r;
   p.bias = bias;
   p.sh = sh->data; p.shb = sh->stride_b; p.shn = sh->stride_n;
   const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -441,8 +463,8 @@ int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys,
 
 int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys, const float* bias,
                  const void* hagg, int64_t groups, const pom_rope* rope, const pom_view* grad_sh,
-                 const pom_view* grad_ys, float* grad_hagg, float* grad_bias, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 const pom_view* grad_ys, const pom_tview* grad_ys_t, float* grad_hagg, float* grad_bias,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   pom::GateParams p;
   int per_token = 0;
   if (int r = check_view(grad_sh, "grad_sh")) return r;
@@ -450,6 +472,7 @@ int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys,
   if (int r = setup_gate(p, per_token, dtype, B, N, P, ys, hagg, groups, rope, {grad_sh, grad_ys})) return r;
   if (!grad_hagg) return fail(POM_ERR_INVALID, "grad_hagg is null");
   if (!aligned(grad_hagg, 4 * p.g.cpt)) return fail(POM_ERR_INVALID, "grad_hagg must be 16-byte aligned");
+  if (int r = set_tview(p.dyst, grad_ys_t, dtype, p.g.cpt, B, N, "grad_ys_t")) return r;
   p.bias = bias;
   p.dsh = grad_sh->data; p.dsb = grad_sh->stride_b; p.dsn = grad_sh->stride_n;
   p.dys = grad_ys->data; p.dyb = grad_ys->stride_b; p.dyn = grad_ys->stride_n;
@@ -462,6 +485,21 @@ int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys,
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::gate_bwd_t<decltype(t)>(p, per_token, st); }),
                     "pom_gate_bwd launch");
+}
+
+int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src, void* dst,
+                  int64_t ld_dst, void* stream) {
+  if (int r = check_dtype(dtype)) return r;
+  if (rows < 0 || cols < 0) return fail(POM_ERR_INVALID, "rows (%lld) and cols (%lld) must be >= 0",
+                                        (long long)rows, (long long)cols);
+  if (rows == 0 || cols == 0) return POM_OK;
+  if (!src || !dst) return fail(POM_ERR_INVALID, "src and dst must be non-null");
+  if (ld_src < cols) return fail(POM_ERR_INVALID, "ld_src (%lld) < cols (%lld)", (long long)ld_src, (long long)cols);
+  if (ld_dst < rows) return fail(POM_ERR_INVALID, "ld_dst (%lld) < rows (%lld)", (long long)ld_dst, (long long)rows);
+  const int eb = elem_bytes(dtype);
+  if (!aligned(src, eb) || !aligned(dst, eb)) return fail(POM_ERR_INVALID, "src and dst must be element-aligned");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return hip_status(pom::transpose_t(eb, src, ld_src, dst, ld_dst, rows, cols, st), "pom_transpose launch");
 }
 
 }  // extern "C"

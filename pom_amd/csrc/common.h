@@ -16,6 +16,7 @@ namespace pom {
 constexpr int kWave = 64;          // CDNA wavefront width
 constexpr int kWaves = 4;          // waves per workgroup in the streaming kernels
 constexpr int kThreads = kWave * kWaves;
+constexpr int kMaxLpr = kWave;      // lanes per token row: 2^lpr_log2 <= one wave
 constexpr int kMaxK = 16;          // highest polynomial degree supported
 
 // ---------------------------------------------------------------------------
@@ -182,8 +183,18 @@ __device__ __forceinline__ float poly_grad_acc(float h, float w, const float (&c
 }
 
 // Hardsigmoid relu6(z + 3) / 6 and its derivative (torch: 1/6 on (-3, 3)).
+// The division by 6 is a product with RN(1/6) plus one fma correction
+// (q = x r, e = x - 6 q exactly, q' = q + e r), three instructions where an
+// IEEE division expands to about ten.  q' equals RN(x / 6) for every x in
+// [2^-122, 6] (checked exhaustively over all fp32 values) and for x = 0; the
+// argument relu6(z + 3) never lies strictly between: z + 3 is 0 or at least
+// ulp(3) / 2 = 2^-23 in magnitude (Sterbenz), so hsig matches torch's
+// relu6(z + 3) / 6 bit for bit.
 __device__ __forceinline__ float hsig(float z) {
-  return fminf(fmaxf(z + 3.0f, 0.0f), 6.0f) / 6.0f;
+  const float x = fminf(fmaxf(z + 3.0f, 0.0f), 6.0f);
+  constexpr float r = 1.0f / 6.0f;
+  const float q = x * r;
+  return __builtin_fmaf(__builtin_fmaf(-q, 6.0f, x), r, q);
 }
 __device__ __forceinline__ float hsig_grad(float z) {
   return (z > -3.0f && z < 3.0f) ? (1.0f / 6.0f) : 0.0f;

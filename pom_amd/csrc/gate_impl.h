@@ -20,7 +20,7 @@
 
 namespace pom {
 
-template <typename T, int CPT, int MODE>
+template <typename T, int CPT, int MODE, bool TR>
 __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, int per_token) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
@@ -32,9 +32,11 @@ __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, 
   int64_t f, rbeg, rend;
   chunk_rows(p.g, chunk, p.N, f, rbeg, rend);
   const int64_t vcol = slab * G.lpr + G.lcol;
-  if (vcol >= p.g.nvec) return;   // no cross-lane work in the forward
+  // Lanes past the channels run the walk on channel 0 (every wave takes part
+  // in the staged channel-major stores) and store nothing.
+  const bool active = vcol < p.g.nvec;
   Map map;
-  map.init(vcol, p.P);
+  map.init(active ? vcol : 0, p.P);
   const int64_t ngroups = per_token ? p.N : p.g.F;
 
   float bias[CPT2], hv[CPT2];
@@ -54,17 +56,27 @@ __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, 
 
   const T* yb = reinterpret_cast<const T*>(p.ys) + b * p.ysb;
   T* ob = reinterpret_cast<T*>(p.sh) + b * p.shb;
-  const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+  const RowWalk W = TR ? RowWalk::consecutive(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U)
+                       : RowWalk(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+  __shared__ __attribute__((aligned(16))) unsigned char tile_raw[TR ? TrTile<U, CPT2>::kElems * sizeof(T) : 16];
+  T* tile = reinterpret_cast<T*>(tile_raw);
 
-  auto step = [&](int64_t base, auto tail_tag) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
+  struct Buf {
     Pack<T, CPT> y1[U], y2[ROPE ? U : 1];
+  };
+  auto load = [&](Buf& bf, int64_t base, bool clamp) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const T* row = yb + W.row(base, u, TAIL) * p.ysn;
-      y1[u].load(row + map.c1);
-      if constexpr (ROPE) y2[u].load(row + map.c2);
+      const T* row = yb + W.row(base, u, clamp) * p.ysn;
+      bf.y1[u].load(row + map.c1);
+      if constexpr (ROPE) bf.y2[u].load(row + map.c2);
     }
+  };
+  auto step = [&](const Buf& bf, int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    float ot[TR ? U : 1][CPT2];
+    const auto& y1 = bf.y1;
+    const auto& y2 = bf.y2;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t n = W.row(base, u, TAIL);
@@ -89,29 +101,44 @@ __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, 
           o1[i] = (a * cs[i] - bb * sn[i]) * hv[i];
           o2[i] = (bb * cs[i] + a * sn[i]) * hv[CPT + i];
         }
-        if (!TAIL || W.valid(base, u)) {
+        if (active && (!TAIL || W.valid(base, u))) {
           VecIO<T, CPT>::store(orow + map.c1, o1);
           VecIO<T, CPT>::store(orow + map.c2, o2);
+        }
+        if constexpr (TR) {
+#pragma unroll
+          for (int i = 0; i < CPT; ++i) {
+            ot[u][i] = o1[i];
+            ot[u][CPT + i] = o2[i];
+          }
         }
       } else {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) o1[i] = hsig(y1[u].get(i) + bias[i]) * hv[i];
-        if (!TAIL || W.valid(base, u)) VecIO<T, CPT>::store(orow + map.c1, o1);
+        if (active && (!TAIL || W.valid(base, u))) VecIO<T, CPT>::store(orow + map.c1, o1);
+        if constexpr (TR) {
+#pragma unroll
+          for (int i = 0; i < CPT; ++i) ot[u][i] = o1[i];
+        }
       }
     }
+    if constexpr (TR) {
+      const int64_t left = W.nrows - base;
+      store_tr_staged<T, U, CPT2>(
+          p.sht, G, b, W.rbeg + base, left < W.step ? left : W.step,
+          [&](int l, int i) { return slab_chan<CPT, MODE>(slab, G.lpr, p.g.nvec, p.P, l, i); }, ot, tile);
+    }
   };
-  const int64_t nfull = W.full_steps();
-  for (int64_t it = 0; it < nfull; ++it) step(it * W.step, std::false_type{});
-  if (W.has_tail()) step(nfull * W.step, std::true_type{});
+  walk_rows<Buf>(W, load, step);
 }
 
-template <typename T, int CPT, int MODE>
+template <typename T, int CPT, int MODE, bool TR>
 __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, int per_token) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
   constexpr int U = ROPE ? 2 : 4;
-  __shared__ float red[kWaves][16 * CPT2];
+  __shared__ float red[kWaves][kMaxLpr * CPT2];
 
   const LaneGeom G(p.g.lpr_log2);
   const int64_t slab = blockIdx.x, chunk = blockIdx.y, b = blockIdx.z;
@@ -136,23 +163,35 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
   const T* yb = reinterpret_cast<const T*>(p.ys) + b * p.ysb;
   const T* gb = reinterpret_cast<const T*>(p.dsh) + b * p.dsb;
   T* dyb = reinterpret_cast<T*>(p.dys) + b * p.dyb;
-  const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+  const RowWalk W = TR ? RowWalk::consecutive(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U)
+                       : RowWalk(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+  __shared__ __attribute__((aligned(16))) unsigned char tile_raw[TR ? TrTile<U, CPT2>::kElems * sizeof(T) : 16];
+  T* tile = reinterpret_cast<T*>(tile_raw);
 
-  auto step = [&](int64_t base, auto tail_tag) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
+  struct Buf {
     Pack<T, CPT> y1[U], y2[ROPE ? U : 1], g1[U], g2[ROPE ? U : 1];
+  };
+  auto load = [&](Buf& bf, int64_t base, bool clamp) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t rr = W.row(base, u, TAIL);
+      const int64_t rr = W.row(base, u, clamp);
       const T* yrow = yb + rr * p.ysn;
       const T* grow = gb + rr * p.dsn;
-      y1[u].load(yrow + map.c1);
-      g1[u].load(grow + map.c1);
+      bf.y1[u].load(yrow + map.c1);
+      bf.g1[u].load(grow + map.c1);
       if constexpr (ROPE) {
-        y2[u].load(yrow + map.c2);
-        g2[u].load(grow + map.c2);
+        bf.y2[u].load(yrow + map.c2);
+        bf.g2[u].load(grow + map.c2);
       }
     }
+  };
+  auto step = [&](const Buf& bf, int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    float dt[TR ? U : 1][CPT2];
+    const auto& y1 = bf.y1;
+    const auto& y2 = bf.y2;
+    const auto& g1 = bf.g1;
+    const auto& g2 = bf.g2;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const bool in = !TAIL || W.valid(base, u);
@@ -198,10 +237,11 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
       for (int i = 0; i < CPT2; ++i) {
         dz[i] = ds[i] * hsig_grad(z[i]);
         db[i] += dz[i];
+        if constexpr (TR) dt[u][i] = dz[i];
       }
       if (per_token) {
         // one token per group: the gradient of hagg is the contribution itself
-        if (in) {
+        if (active && in) {
           float* drow = p.dhagg + (b * p.N + n) * p.P;
           float t[CPT];
 #pragma unroll
@@ -217,7 +257,7 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
 #pragma unroll
         for (int i = 0; i < CPT2; ++i) dh[i] += dcon[i];
       }
-      if (in) {
+      if (active && in) {
         T* drow = dyb + n * p.dyn;
         float t[CPT];
 #pragma unroll
@@ -230,12 +270,16 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
         }
       }
     }
+    if constexpr (TR) {
+      const int64_t left = W.nrows - base;
+      store_tr_staged<T, U, CPT2>(
+          p.dyst, G, b, W.rbeg + base, left < W.step ? left : W.step,
+          [&](int l, int i) { return slab_chan<CPT, MODE>(slab, G.lpr, p.g.nvec, p.P, l, i); }, dt, tile);
+    }
   };
-  if (active) {
-    const int64_t nfull = W.full_steps();
-    for (int64_t it = 0; it < nfull; ++it) step(it * W.step, std::false_type{});
-    if (W.has_tail()) step(nfull * W.step, std::true_type{});
-  }
+  // every lane walks (lanes past the channels on channel 0, storing nothing):
+  // the staged channel-major stores synchronise the workgroup
+  walk_rows<Buf>(W, load, step);
 
   // Chunk partials: dhagg (unless per-token) and dbias.
   const int nslot = G.lpr * CPT2;
@@ -292,13 +336,35 @@ static __global__ void __launch_bounds__(kThreads) gate_bwd_finalize(const GateP
   }
 }
 
-template <typename T, int CPT>
-hipError_t gate_fwd_cpt(const GateParams& p, hipStream_t st, int per_token) {
+template <typename T, int CPT, bool TR>
+hipError_t gate_fwd_tr(const GateParams& p, hipStream_t st, int per_token) {
   const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
   switch (p.mode) {
-    case MODE_PLAIN: hipLaunchKernelGGL((gate_fwd_kernel<T, CPT, MODE_PLAIN>), grid, block, 0, st, p, per_token); break;
-    case MODE_ROPE1D: hipLaunchKernelGGL((gate_fwd_kernel<T, CPT, MODE_ROPE1D>), grid, block, 0, st, p, per_token); break;
-    case MODE_ROPE2D: hipLaunchKernelGGL((gate_fwd_kernel<T, CPT, MODE_ROPE2D>), grid, block, 0, st, p, per_token); break;
+    case MODE_PLAIN: hipLaunchKernelGGL((gate_fwd_kernel<T, CPT, MODE_PLAIN, TR>), grid, block, 0, st, p, per_token); break;
+    case MODE_ROPE1D: hipLaunchKernelGGL((gate_fwd_kernel<T, CPT, MODE_ROPE1D, TR>), grid, block, 0, st, p, per_token); break;
+    case MODE_ROPE2D: hipLaunchKernelGGL((gate_fwd_kernel<T, CPT, MODE_ROPE2D, TR>), grid, block, 0, st, p, per_token); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename T, int CPT>
+hipError_t gate_fwd_cpt(const GateParams& p, hipStream_t st, int per_token) {
+  if constexpr (kTrBuilt<T, CPT>) {
+    if (p.sht.data) return gate_fwd_tr<T, CPT, true>(p, st, per_token);
+  } else {
+    if (p.sht.data) return hipErrorInvalidValue;
+  }
+  return gate_fwd_tr<T, CPT, false>(p, st, per_token);
+}
+
+template <typename T, int CPT, bool TR>
+hipError_t gate_bwd_tr(const GateParams& p, hipStream_t st, int per_token) {
+  const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
+  switch (p.mode) {
+    case MODE_PLAIN: hipLaunchKernelGGL((gate_bwd_kernel<T, CPT, MODE_PLAIN, TR>), grid, block, 0, st, p, per_token); break;
+    case MODE_ROPE1D: hipLaunchKernelGGL((gate_bwd_kernel<T, CPT, MODE_ROPE1D, TR>), grid, block, 0, st, p, per_token); break;
+    case MODE_ROPE2D: hipLaunchKernelGGL((gate_bwd_kernel<T, CPT, MODE_ROPE2D, TR>), grid, block, 0, st, p, per_token); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -306,14 +372,12 @@ hipError_t gate_fwd_cpt(const GateParams& p, hipStream_t st, int per_token) {
 
 template <typename T, int CPT>
 hipError_t gate_bwd_cpt(const GateParams& p, hipStream_t st, int per_token) {
-  const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
-  switch (p.mode) {
-    case MODE_PLAIN: hipLaunchKernelGGL((gate_bwd_kernel<T, CPT, MODE_PLAIN>), grid, block, 0, st, p, per_token); break;
-    case MODE_ROPE1D: hipLaunchKernelGGL((gate_bwd_kernel<T, CPT, MODE_ROPE1D>), grid, block, 0, st, p, per_token); break;
-    case MODE_ROPE2D: hipLaunchKernelGGL((gate_bwd_kernel<T, CPT, MODE_ROPE2D>), grid, block, 0, st, p, per_token); break;
-    default: return hipErrorInvalidValue;
+  if constexpr (kTrBuilt<T, CPT>) {
+    if (p.dyst.data) return gate_bwd_tr<T, CPT, true>(p, st, per_token);
+  } else {
+    if (p.dyst.data) return hipErrorInvalidValue;
   }
-  return hipGetLastError();
+  return gate_bwd_tr<T, CPT, false>(p, st, per_token);
 }
 
 // per_token: hagg holds one row per token (token-causal aggregation).

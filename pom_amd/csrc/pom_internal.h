@@ -46,6 +46,13 @@ struct Geom {
   int64_t nch = 1;      // chunks per batch row = F * cpf
 };
 
+// Optional channel-major ("transposed") copy of a (B, N, P) output:
+// element (b, n, c) at data[c * ld + b * sb + n].  data == nullptr: none.
+struct TrOut {
+  void* data = nullptr;
+  int64_t ld = 0, sb = 0;
+};
+
 struct AggParams {
   int dtype = DT_BF16;
   int mode = MODE_PLAIN;
@@ -76,6 +83,7 @@ struct AggParams {
   const float* wf = nullptr;      // (B, F, P) fp32 per-frame token weights (F > 1)
   void* gx = nullptr;             // (B, N, P) view, unit channel stride
   int64_t sgb = 0, sgn = 0;
+  TrOut gxt;                      // channel-major copy of gx, or none
   float* gc = nullptr;            // (P, K) fp32
 
   // workspace
@@ -132,11 +140,13 @@ struct GateParams {
 
   void* sh = nullptr;             // (B, N, P) output view (forward)
   int64_t shb = 0, shn = 0;
+  TrOut sht;                      // channel-major copy of sh, or none
 
   const void* dsh = nullptr;      // (B, N, P) upstream gradient view (backward)
   int64_t dsb = 0, dsn = 0;
   void* dys = nullptr;            // (B, N, P) gradient of y_s (backward)
   int64_t dyb = 0, dyn = 0;
+  TrOut dyst;                     // channel-major copy of dys, or none
   float* dhagg = nullptr;         // (B, G, P) fp32
   float* dbias = nullptr;         // (P,) fp32 or null
 
@@ -147,5 +157,9 @@ struct GateParams {
 // per_token: hagg holds one row per token (token-causal aggregation).
 template <typename T> hipError_t gate_fwd_t(const GateParams& p, int per_token, hipStream_t st);
 template <typename T> hipError_t gate_bwd_t(const GateParams& p, int per_token, hipStream_t st);
+
+// dst (C x R, row stride ldd) = src^T (R x C, row stride lds); elements of elem_bytes (2 or 4).
+hipError_t transpose_t(int elem_bytes, const void* src, int64_t lds, void* dst, int64_t ldd, int64_t R, int64_t C,
+                       hipStream_t st);
 
 }  // namespace pom

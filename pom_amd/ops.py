@@ -19,6 +19,7 @@ and its backward writes grad_x straight into the matching half of dY.
 from __future__ import annotations
 
 import ctypes
+import os
 import weakref
 from typing import Optional, Tuple
 
@@ -56,6 +57,30 @@ class _Span:
         return False
 
 
+# The backward GEMMs in 16-bit types run on operands that are contiguous along
+# the reduction dimension (x^T, g^T, sh^T, dY^T for the weight gradients and
+# the transposed weights for the data gradients), which the matrix-core GEMMs
+# run markedly faster than the strided forms.  POM_AMD_NT_GEMMS=0 disables.
+_NT_GEMMS = os.environ.get("POM_AMD_NT_GEMMS", "1") != "0"
+
+# How the token-contiguous copies of sh and dY are made: "fused" (default)
+# has the gate / aggregation kernels write them in the same pass (pom_tview
+# outputs); "side" transposes them on a second stream (default priority)
+# while the next GEMM runs on the current one.  Fused measured faster: the
+# overlapped copies slow the concurrent GEMMs by more than they save.  x^T and
+# g^T (inputs of the layer) are always transposed on the second stream.
+_NT_COPIES = os.environ.get("POM_AMD_NT_COPIES", "fused")
+_copy_streams: dict = {}
+
+
+def _copy_stream(device: torch.device) -> torch.cuda.Stream:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _copy_streams.get(idx)
+    if s is None:
+        s = _copy_streams[idx] = torch.cuda.Stream(device=idx)
+    return s
+
+
 def _check_degree(k: int) -> None:
     if k > _lib.MAX_DEGREE:
         raise NotImplementedError(f"pom_amd kernels support degree k <= {_lib.MAX_DEGREE} (got {k})")
@@ -64,29 +89,97 @@ def _check_degree(k: int) -> None:
 
 
 _f32_cache: dict = {}
+_wt_cache: dict = {}
 
 
-def _as_f32(t: torch.Tensor) -> torch.Tensor:
-    """fp32 contiguous copy of a small parameter (coefficients, gate bias), kept
-    while that same tensor object is alive and unchanged (identity, storage
-    pointer and version counter), so a bf16 model does not pay a conversion
-    kernel per call.  Keyed by object identity: a freed tensor's address or id
-    reused by a new tensor can never hit a stale copy."""
-    if t.dtype == torch.float32 and t.is_contiguous():
-        return t.detach()
-    hit = _f32_cache.get(id(t))
+def _derived(cache: dict, t: torch.Tensor, make):
+    """``make(t)``, kept while that same tensor object is alive and unchanged
+    (identity, storage pointer and version counter), so a parameter's derived
+    copy is not rebuilt per call while the parameter does not change.  Keyed
+    by object identity: a freed tensor's address or id reused by a new tensor
+    can never hit a stale copy.  Under stream capture the copy is always
+    rebuilt, so a captured graph recomputes it on every replay (a replay runs
+    no Python and would otherwise keep the capture-time copy)."""
+    if torch.cuda.is_current_stream_capturing():
+        return make(t)
+    hit = cache.get(id(t))
     if hit is not None:
         ref, version, ptr, c = hit
         if ref() is t and version == t._version and ptr == t.data_ptr():
             return c
-    c = t.detach().float().contiguous()
-    if len(_f32_cache) > 64:
-        for k in [k for k, v in _f32_cache.items() if v[0]() is None]:
-            del _f32_cache[k]
-        if len(_f32_cache) > 64:
-            _f32_cache.clear()
-    _f32_cache[id(t)] = (weakref.ref(t), t._version, t.data_ptr(), c)
+    c = make(t)
+    if len(cache) > 64:
+        for k in [k for k, v in cache.items() if v[0]() is None]:
+            del cache[k]
+        if len(cache) > 64:
+            cache.clear()
+    cache[id(t)] = (weakref.ref(t), t._version, t.data_ptr(), c)
     return c
+
+
+def _as_f32(t: torch.Tensor) -> torch.Tensor:
+    """fp32 contiguous copy of a small parameter (coefficients, gate bias),
+    cached per parameter version so a bf16 model does not pay a conversion
+    kernel per call."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.detach()
+    return _derived(_f32_cache, t, lambda u: u.detach().float().contiguous())
+
+
+def transpose(t: torch.Tensor, name: str = "transpose") -> torch.Tensor:
+    """Contiguous (C, R) copy of a 2-D (R, C) tensor with unit column stride,
+    on the HIP transpose kernel (pom_transpose)."""
+    _lib.require_device(t)
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1):
+        raise ValueError(f"transpose needs a 2-D tensor with unit column stride, got {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    lib = _lib.load()
+    R, C = t.shape
+    out = torch.empty(C, R, dtype=t.dtype, device=t.device)
+    with _Span(name):
+        rc = lib.pom_transpose(dtype_code(t), R, C, t.data_ptr(), max(t.stride(0), C), out.data_ptr(), R,
+                               stream_handle(t.device))
+    check(rc, "pom_transpose")
+    return out
+
+
+def invalidate_derived() -> None:
+    """Drop every cached parameter-derived copy (fp32 coefficients, transposed
+    weights), as an optimizer update of all parameters would."""
+    _f32_cache.clear()
+    _wt_cache.clear()
+
+
+def _transpose_into(src: torch.Tensor, dst: torch.Tensor, name: str) -> None:
+    """dst (C, R) <- src (R, C)^T; both 2-D with unit inner stride."""
+    R, C = src.shape
+    with _Span(name):
+        rc = _lib.load().pom_transpose(dtype_code(src), R, C, src.data_ptr(), max(src.stride(0), C),
+                                       dst.data_ptr(), dst.stride(0), stream_handle(src.device))
+    check(rc, "pom_transpose")
+
+
+def _with_copy(call, out_t, src_rows: torch.Tensor, name: str, what: str, B: int, N: int) -> None:
+    """Run a launch that can also write a channel-major copy ``out_t`` of its
+    (B, N, C) output.  ``call(tv)`` launches with tv (a PomTView pointer or
+    None) and returns the status.  When the kernels do not build the copy for
+    this shape (POM_ERR_UNSUPPORTED, raised before any launch), the launch runs
+    without it and the copy is made from ``src_rows`` (the output as (B*N, C))
+    by the transpose kernel."""
+    if out_t is None:
+        check(call(None), what)
+        return
+    rc = call(_lib.tview(out_t, B, N))
+    if rc == _lib.POM_ERR_UNSUPPORTED:
+        check(call(None), what)
+        _transpose_into(src_rows, out_t, name)
+        return
+    check(rc, what)
+
+
+def _weight_t(w: torch.Tensor) -> torch.Tensor:
+    """Transposed copy of a projection weight, cached per weight version."""
+    return _derived(_wt_cache, w, lambda u: transpose(u.detach(), "transpose_w"))
 
 
 def _coeff32(coeff: torch.Tensor, p: int, k: int) -> torch.Tensor:
@@ -129,8 +222,11 @@ def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
 def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int, go32: torch.Tensor,
                  grad_x: torch.Tensor, mask32: Optional[torch.Tensor] = None,
                  count: Optional[torch.Tensor] = None, n_past: int = 0,
-                 rope: Optional[RopeSpec] = None) -> torch.Tensor:
-    """Launch pom_agg_bwd; writes grad_x in place and returns grad_coeff (P, K) fp32."""
+                 rope: Optional[RopeSpec] = None, grad_x_t: Optional[torch.Tensor] = None,
+                 grad_x_rows: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Launch pom_agg_bwd; writes grad_x in place (and, when given, its
+    channel-major copy grad_x_t (P, B*N); grad_x_rows is grad_x as (B*N, P))
+    and returns grad_coeff (P, K) fp32."""
     lib = _lib.load()
     B, N, P = x.shape
     dt = dtype_code(x)
@@ -140,13 +236,14 @@ def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     ws = workspace(x.device, nbytes)
     xv, gv = view3(x), view3(grad_x)
     go32 = go32.float().contiguous()
-    with _Span("agg_bwd"):
-        rc = lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
-                             mask32.stride(0) if mask32 is not None else 0,
-                             mask32.stride(1) if mask32 is not None else 0, ptr(count),
-                             frame_len, n_past, rope_ptr(rope), go32.data_ptr(), ctypes.byref(gv),
-                             gc.data_ptr(), ws.data_ptr(), ws.numel(), stream_handle(x.device))
-    check(rc, "pom_agg_bwd")
+    def call(tv):
+        with _Span("agg_bwd"):
+            return lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+                                   mask32.stride(0) if mask32 is not None else 0,
+                                   mask32.stride(1) if mask32 is not None else 0, ptr(count),
+                                   frame_len, n_past, rope_ptr(rope), go32.data_ptr(), ctypes.byref(gv), tv,
+                                   gc.data_ptr(), ws.data_ptr(), ws.numel(), stream_handle(x.device))
+    _with_copy(call, grad_x_t, grad_x_rows, "transpose_dy", "pom_agg_bwd", B, N)
     return gc
 
 
@@ -158,25 +255,33 @@ def _hagg(hagg: torch.Tensor, ys: torch.Tensor) -> torch.Tensor:
 
 
 def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.Tensor,
-                 rope: Optional[RopeSpec] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """sh = R hardsigmoid(ys + bias) * hagg[group], via pom_gate_fwd."""
+                 rope: Optional[RopeSpec] = None, out: Optional[torch.Tensor] = None,
+                 out_t: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sh = R hardsigmoid(ys + bias) * hagg[group], via pom_gate_fwd; with
+    out_t (P, B*N), also its channel-major copy."""
     lib = _lib.load()
     B, N, P = ys.shape
     hagg = _hagg(hagg, ys)
     G = hagg.shape[1]
     sh = torch.empty(B, N, P, dtype=ys.dtype, device=ys.device) if out is None else out
     yv, sv = view3(ys), view3(sh)
-    with _Span("gate_fwd"):
-        rc = lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
-                              rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
-    check(rc, "pom_gate_fwd")
+
+    def call(tv):
+        with _Span("gate_fwd"):
+            return lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
+                                    rope_ptr(rope), ctypes.byref(sv), tv, stream_handle(ys.device))
+    _with_copy(call, out_t, sh.view(B * N, P) if out_t is not None else None, "transpose_sh", "pom_gate_fwd",
+               B, N)
     return sh
 
 
 def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.Tensor,
                   grad_sh: torch.Tensor, grad_ys: torch.Tensor, rope: Optional[RopeSpec] = None,
-                  want_bias: bool = True):
-    """Writes grad_ys in place; returns (grad_hagg (B, G, P) fp32, grad_bias (P,) fp32 or None)."""
+                  want_bias: bool = True, grad_ys_t: Optional[torch.Tensor] = None,
+                  grad_ys_rows: Optional[torch.Tensor] = None):
+    """Writes grad_ys in place (and, when given, its channel-major copy
+    grad_ys_t (P, B*N); grad_ys_rows is grad_ys as (B*N, P)); returns
+    (grad_hagg (B, G, P) fp32, grad_bias (P,) fp32 or None)."""
     lib = _lib.load()
     B, N, P = ys.shape
     hagg = _hagg(hagg, ys)
@@ -188,11 +293,12 @@ def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.
     nbytes = lib.pom_gate_workspace_size(dt, B, N, P, G, rk)
     ws = workspace(ys.device, nbytes)
     yv, gv, dv = view3(ys), view3(grad_sh), view3(grad_ys)
-    with _Span("gate_bwd"):
-        rc = lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
-                              rope_ptr(rope), ctypes.byref(gv), ctypes.byref(dv), gh.data_ptr(), ptr(gb),
-                              ws.data_ptr(), ws.numel(), stream_handle(ys.device))
-    check(rc, "pom_gate_bwd")
+    def call(tv):
+        with _Span("gate_bwd"):
+            return lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
+                                    rope_ptr(rope), ctypes.byref(gv), ctypes.byref(dv), tv, gh.data_ptr(),
+                                    ptr(gb), ws.data_ptr(), ws.numel(), stream_handle(ys.device))
+    _with_copy(call, grad_ys_t, grad_ys_rows, "transpose_dy", "pom_gate_bwd", B, N)
     return gh, gb
 
 
@@ -339,17 +445,37 @@ class _PoMLayer(torch.autograd.Function):
       backward: dsh = g W_ag (T, P); dY (T, 2P) is filled in two halves by the
                 gate (s-half) and aggregation (h-half) kernels, then
                 dx = dY W_qc and dW_qc = dY^T x.
-    Saved: x, Y, sh, hagg (fp32), the fp32 coefficient/bias copies.
+    In 16-bit training (_NT_GEMMS) the weight gradients are dW_ag = g^T sh
+    and dW_qc = dY^T x on token-contiguous copies (gt, sht, dyt, xt) and the
+    data gradients use transposed weights, so every backward GEMM has both
+    operands contiguous in K.  The copies of inputs (x, g) are made on a
+    second stream while the current one runs the GEMM that does not need
+    them; sh^T and dY^T likewise ("side") or inside the producing kernels
+    ("fused").
+    Saved: Y, hagg, the fp32 coefficient/bias copies, and x, sh (or x^T, sh^T).
     Returns (out, hagg) — hagg in x.dtype, differentiable (state_forward's carry).
     """
 
     @staticmethod
-    def forward(ctx, x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, mask, rope_h, rope_s, carry, n_past):
+    def forward(ctx, x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, mask, rope_h, rope_s, carry, n_past,
+                training):
         _lib.require_device(x)
         B, N, D = x.shape
         P = coeff.shape[0]
+        T = B * N
         dt = x.dtype
-        x2 = x.reshape(B * N, D)
+        dev = x.device
+        x2 = x.reshape(T, D)
+        nt = training and _NT_GEMMS and dt != torch.float32
+        want_xt = nt and ctx.needs_input_grad[1]
+        want_sht = nt and ctx.needs_input_grad[4]
+        cur = torch.cuda.current_stream(dev)
+        side = _copy_stream(dev) if (want_xt or want_sht) else None
+        xt = sht = None
+        if want_xt:
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                xt = transpose(x2, "transpose_x")                  # (D, T), overlaps qc_fwd
         wq = w_qc if w_qc.dtype == dt else w_qc.to(dt)
         with _Span("gemm_qc_fwd"), tuned_gemms():
             y = torch.mm(x2, wq.t())                                # (T, 2P)
@@ -358,13 +484,30 @@ class _PoMLayer(torch.autograd.Function):
         c32 = _coeff32(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
         b32 = _as_f32(se_bias)
-        sh = gate_forward(s_view, b32, hagg, rope_s)                # (B, N, P)
+        fused = want_sht and _NT_COPIES == "fused"
+        if fused:
+            sht = torch.empty(P, T, dtype=dt, device=dev)
+        sh = gate_forward(s_view, b32, hagg, rope_s, out_t=sht if fused else None)   # (B, N, P)
+        if want_sht and not fused:
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                sht = transpose(sh.view(T, P), "transpose_sh")      # (P, T), overlaps ag_fwd
         wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
         with _Span("gemm_ag_fwd"), tuned_gemms():
-            out = torch.mm(sh.view(B * N, P), wa.t())
+            out = torch.mm(sh.view(T, P), wa.t())
         if b_ag is not None:
             out = out + b_ag.to(dt)
-        ctx.save_for_backward(x, y, sh, hagg, c32, b32, wq, wa, mask, count)
+        if side is not None:
+            # join before x or sh can be freed; the copies live on the current stream
+            cur.wait_stream(side)
+            if xt is not None:
+                xt.record_stream(cur)
+            if sht is not None and not fused:
+                sht.record_stream(cur)
+        ctx.nt = nt
+        ctx.save_for_backward(None if want_xt else x, xt, y, None if want_sht else sh, sht,
+                              hagg, c32, b32, wq, wa, mask, count)
+        ctx.shape = (B, N, D)
         ctx.set_materialize_grads(False)   # the aggregate output is usually unused
         ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None)
         ctx.dtypes = (w_qc.dtype, se_bias.dtype, coeff.dtype, w_ag.dtype,
@@ -373,41 +516,86 @@ class _PoMLayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out, grad_hagg):
-        x, y, sh, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
+        x, xt, y, sh, sht, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
         k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias = ctx.meta
-        B, N, D = x.shape
+        B, N, D = ctx.shape
+        dev = y.device
+        dt = y.dtype
         if grad_out is None:   # only the aggregate was used downstream
-            grad_out = torch.zeros(B, N, D, dtype=x.dtype, device=x.device)
+            grad_out = torch.zeros(B, N, D, dtype=dt, device=dev)
         P = c32.shape[0]
         T = B * N
-        dt = x.dtype
+        need_x, need_wq, need_wa = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[4]
+        nt_a = xt is not None or sht is not None   # token-contiguous weight gradients
+        nt = ctx.nt
         g2 = grad_out.reshape(T, D)
         if g2.dtype != dt:
             g2 = g2.to(dt)
+        if nt and not g2.is_contiguous():
+            g2 = g2.contiguous()
+        cur = torch.cuda.current_stream(dev)
+        side = _copy_stream(dev) if nt_a else None
+        gt = None
+        if need_wa and sht is not None:
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                gt = transpose(g2, "transpose_g")                  # (D, T), overlaps ag_dgrad
         with _Span("gemm_ag_dgrad"), tuned_gemms():
-            dsh = torch.mm(g2, wa)                                  # (T, P)
-        with _Span("gemm_ag_wgrad"), tuned_gemms():
-            dw_ag = torch.mm(g2.t(), sh.view(T, P))                 # (D, P)
+            dsh = torch.mm(g2, _weight_t(wa).t()) if nt else torch.mm(g2, wa)   # (T, P)
+        dw_ag = None
+        if need_wa:
+            if gt is not None:
+                cur.wait_stream(side)
+                gt.record_stream(cur)
+                with _Span("gemm_ag_wgrad"), tuned_gemms():
+                    dw_ag = torch.mm(gt, sht.t())                   # (D, P)
+                del gt
+            else:
+                with _Span("gemm_ag_wgrad"), tuned_gemms():
+                    dw_ag = torch.mm(g2.t(), sh.view(T, P))         # (D, P)
         db_ag = g2.float().sum(0) if has_bias else None
         y3 = y.view(B, N, 2 * P)
-        dy = torch.empty(T, 2 * P, dtype=dt, device=x.device)
+        dy = torch.empty(T, 2 * P, dtype=dt, device=dev)
         dy3 = dy.view(B, N, 2 * P)
-        dh, dbias = gate_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), dy3[..., P:], rope_s)
+        want_dyt = need_wq and xt is not None
+        fused = want_dyt and _NT_COPIES == "fused"
+        dyt = torch.empty(2 * P, T, dtype=dt, device=dev) if fused else None
+        dh, dbias = gate_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), dy3[..., P:], rope_s,
+                                  grad_ys_t=None if dyt is None else dyt[P:], grad_ys_rows=dy[:, P:])
         if grad_hagg is not None:
             dh = dh + grad_hagg.float()
-        dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h)
-        with _Span("gemm_qc_dgrad"), tuned_gemms():
-            dx = torch.mm(dy, wq)                                   # (T, D)
-        with _Span("gemm_qc_wgrad"), tuned_gemms():
-            dw_qc = torch.mm(dy.t(), x.reshape(T, D))               # (2P, D)
+        dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h,
+                              grad_x_t=None if dyt is None else dyt[:P], grad_x_rows=dy[:, :P])
+        if want_dyt and not fused:
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                dyt = transpose(dy, "transpose_dy")                # (2P, T), overlaps qc_dgrad
+        dx = None
+        if need_x:
+            with _Span("gemm_qc_dgrad"), tuned_gemms():
+                dx = torch.mm(dy, _weight_t(wq).t()) if nt else torch.mm(dy, wq)   # (T, D)
+        dw_qc = None
+        if need_wq:
+            if want_dyt:
+                if not fused:
+                    cur.wait_stream(side)
+                    dyt.record_stream(cur)
+                with _Span("gemm_qc_wgrad"), tuned_gemms():
+                    dw_qc = torch.mm(dyt, xt.t())                   # (2P, D)
+            else:
+                with _Span("gemm_qc_wgrad"), tuned_gemms():
+                    dw_qc = torch.mm(dy.t(), x.reshape(T, D))       # (2P, D)
+        if side is not None:
+            cur.wait_stream(side)   # join before g2 or dy can be freed
         g_carry = None
         if has_carry:
             nf = dh.shape[1]
-            w = n_past / (n_past + torch.arange(nf, device=x.device, dtype=torch.float32) + 1.0)
+            w = n_past / (n_past + torch.arange(nf, device=dev, dtype=torch.float32) + 1.0)
             g_carry = (dh * w.view(1, nf, 1)).sum(dim=1, keepdim=True).to(dt)
         tq, tb, tc, ta, tab = ctx.dtypes
-        return (dx.view(B, N, D), dw_qc.to(tq), dbias.to(tb), dcoeff.to(tc), dw_ag.to(ta),
-                None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None)
+        return (None if dx is None else dx.view(B, N, D), None if dw_qc is None else dw_qc.to(tq),
+                dbias.to(tb), dcoeff.to(tc), None if dw_ag is None else dw_ag.to(ta),
+                None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None, None)
 
 
 def pom_layer(x, w_qc, se_bias, coeff, w_ag, b_ag, k: int, frame_len: Optional[int] = None,
@@ -424,4 +612,4 @@ def pom_layer(x, w_qc, se_bias, coeff, w_ag, b_ag, k: int, frame_len: Optional[i
         raise ValueError(f"frame_len {frame_len} must divide the sequence length {N}")
     m32 = None if mask is None else _mask32(mask, x)
     return _PoMLayer.apply(x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, m32, rope_h, rope_s,
-                           carry, n_past if carry is not None else 0)
+                           carry, n_past if carry is not None else 0, torch.is_grad_enabled())

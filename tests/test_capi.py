@@ -32,7 +32,7 @@ def lib():
 def test_header_lists_expected_entry_points():
     names = _declared_functions()
     for n in ["pom_abi_version", "pom_last_error", "pom_agg_workspace_size", "pom_agg_fwd", "pom_agg_bwd",
-              "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd"]:
+              "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd", "pom_transpose"]:
         assert n in names
 
 
@@ -117,8 +117,20 @@ def test_validation_errors_before_launch(lib):
     assert rc == _lib.POM_ERR_INVALID and b"even" in lib.pom_last_error()
     # gate: groups not dividing N
     rc = lib.pom_gate_fwd(1, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 3, None,
-                          ctypes.byref(_view(4096, 1024, 64)), None)
+                          ctypes.byref(_view(4096, 1024, 64)), None, None)
     assert rc == _lib.POM_ERR_INVALID
+    # channel-major copy: fp32 is not built, overlapping strides are rejected, token-causal has none
+    sh = ctypes.byref(_view(4096, 1024, 64))
+    tv = ctypes.byref(_lib.PomTView(8192, 32, 16))
+    rc = lib.pom_gate_fwd(0, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 1, None, sh, tv, None)
+    assert rc == _lib.POM_ERR_UNSUPPORTED and b"16-bit" in lib.pom_last_error()
+    bad = ctypes.byref(_lib.PomTView(8192, 20, 16))   # stride_c < (B-1)*stride_b + N
+    rc = lib.pom_gate_fwd(1, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 1, None, sh, bad, None)
+    assert rc == _lib.POM_ERR_INVALID and b"overlap" in lib.pom_last_error()
+    rc = lib.pom_agg_bwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, None, 1, 0, None,
+                         ctypes.c_void_p(2048), ctypes.byref(_view(4096, 1024, 64)), tv, ctypes.c_void_p(1024),
+                         ws, 1 << 20, None)
+    assert rc == _lib.POM_ERR_UNSUPPORTED and b"token-causal" in lib.pom_last_error()
 
 
 def test_python_errors_without_gpu():
@@ -169,3 +181,16 @@ def test_module_parameters_match_reference_names_and_init():
     sd = r.state_dict()
     r2 = pom_amd.PoMRoPE(32, 2, 2, rope_2d=True)
     r2.load_state_dict(sd, strict=True)
+
+
+def test_transpose_validation_before_launch(lib):
+    from pom_amd import _lib
+    src, dst = ctypes.c_void_p(256), ctypes.c_void_p(4096)
+    assert lib.pom_transpose(1, -1, 4, src, 4, dst, 1, None) == _lib.POM_ERR_INVALID
+    assert lib.pom_transpose(1, 4, 8, src, 4, dst, 4, None) == _lib.POM_ERR_INVALID   # ld_src < cols
+    assert b"ld_src" in lib.pom_last_error()
+    assert lib.pom_transpose(1, 4, 8, src, 8, dst, 2, None) == _lib.POM_ERR_INVALID   # ld_dst < rows
+    assert lib.pom_transpose(1, 4, 8, None, 8, dst, 4, None) == _lib.POM_ERR_INVALID
+    assert lib.pom_transpose(9, 4, 8, src, 8, dst, 4, None) == _lib.POM_ERR_INVALID   # bad dtype
+    assert lib.pom_transpose(1, 4, 8, ctypes.c_void_p(257), 8, dst, 4, None) == _lib.POM_ERR_INVALID
+    assert lib.pom_transpose(1, 0, 8, src, 8, dst, 0, None) == _lib.POM_OK            # empty: no launch

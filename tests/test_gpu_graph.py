@@ -1,7 +1,9 @@
 """A PoM layer forward + backward captured in a HIP graph replays to the
 eager results, bit for bit, across several replays with eager work and
 synchronisations in between (no memset nodes: the kernels' scratch needs no
-initialisation)."""
+initialisation), and after an in-place update of every parameter (the
+graph must recompute the parameter-derived copies, fp32 coefficients and
+transposed weights, on each replay)."""
 import pytest
 import torch
 
@@ -66,3 +68,13 @@ def test_layer_graph_replays_match_eager(device, variant):
         # eager work between replays, then compare again
         eager()
         torch.cuda.synchronize()
+    # an optimizer-like in-place update of every parameter between replays
+    with torch.no_grad():
+        for i, p in enumerate(params):
+            p.mul_(0.75 + 0.05 * i)
+    ref2 = eager()
+    graph.replay()
+    torch.cuda.synchronize()
+    got = [out, x.grad] + [p.grad for p in params]
+    for a, b in zip(got, ref2):
+        assert torch.equal(a, b), "replay after parameter update"
