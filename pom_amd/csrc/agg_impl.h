@@ -419,13 +419,18 @@ static __global__ void __launch_bounds__(kThreads) agg_frame_weights(const AggPa
 // Backward chunk kernel: grad_x for every row of the chunk (written into a
 // strided view, e.g. the h-half of dY) and the chunk's grad_coeff partial.
 // ---------------------------------------------------------------------------
+// Three waves per SIMD: the kernel is memory-bound and latency-limited; the
+// register cap costs at most a few bytes of spill in the plain mode.  With the
+// channel-major copy a lane holds U x CPT2 output values until the staged
+// store, so that variant walks 4 rows per lane instead of 8 to fit the cap.
 template <typename T, int CPT, int KM, int MODE, bool TR>
-__global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+agg_bwd_chunk(const AggParams p) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
   constexpr bool MASKED = MODE == MODE_MASKED;
-  constexpr int U = Mode_<MODE>::U;
+  constexpr int U = TR && !ROPE ? 4 : Mode_<MODE>::U;
   __shared__ float red[kWaves][kMaxLpr * CPT2];
 
   const LaneGeom G(p.g.lpr_log2);
