@@ -65,6 +65,10 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"),
                     help="turn four rocprofv3 --pmc databases (FETCH_SIZE and WRITE_SIZE of a bench run and "
                          "of a --copy-calib run) into per-kernel HBM traffic; writes profiles/traffic_<config>.json")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="summarise a rocprofv3 --kernel-trace --stats --output-format csv directory "
+                         "(run_kernel_stats.csv, run_kernel_trace.csv) of a bench run: per-kernel calls and "
+                         "average duration, projection GEMMs labelled by dispatch order")
     ap.add_argument("--copy-calib", type=float, default=0.0,
                     help="instead of the layer, run a plain device copy of this many MiB "
                          "(calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -231,7 +235,10 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
         torch.cuda.synchronize()
         for name, s, e in ops.kernel_timer:
             per.setdefault(name, []).append(s.elapsed_time(e) * 1e-3)   # seconds
-        dominant = max(per, key=lambda k: sum(per[k]))
+        # copies on the second stream overlap the GEMMs: their event spans
+        # include the wait for free compute units, so they are reported but
+        # never taken as the dominant kernel
+        dominant = max((k for k in per if k not in OVERLAPPED), key=lambda k: sum(per[k]))
         # the timed region records events around the dominant kernel only
         # (events around every launch would add ~5 % to the step)
         ops.kernel_timer = []
@@ -329,11 +336,15 @@ def cpu_run(cfg, budget_s: float):
 
 
 # rocprofv3 kernel names of the launch groups bench.py times
+# launch groups that run on the layer's second stream, concurrently with a GEMM
+OVERLAPPED = {"transpose_x", "transpose_g"}
+
 KERNEL_NAMES = {
     "agg_fwd": ["agg_fwd_chunk", "agg_fwd_finalize"],
     "agg_bwd": ["agg_bwd_chunk", "coeff_grad_finalize", "agg_frame_weights"],
     "gate_fwd": ["gate_fwd_kernel"],
     "gate_bwd": ["gate_bwd_kernel", "gate_bwd_finalize"],
+    "transpose": ["transpose_blocks", "transpose_elems"],   # x^T, g^T and the weights, per step
 }
 
 
@@ -353,27 +364,30 @@ def _pmc_per_kernel(db: str, counter: str):
 COPY_CALIB_MIB = 144   # pmc_summary expects the calibration run made with --copy-calib 144
 
 
-def _gemm_groups(db: str):
-    """Library kernel name of each projection GEMM, from the dispatch order of
-    one layer step: qc_fwd precedes agg_fwd_chunk, ag_fwd follows gate_fwd,
-    ag_dgrad and ag_wgrad precede gate_bwd, qc_dgrad and qc_wgrad follow
-    coeff_grad_finalize."""
+def _gemm_dispatches(db: str):
+    """Dispatch id and library kernel name of each projection GEMM of the last
+    complete fwd+bwd step, from the dispatch order: qc_fwd precedes
+    agg_fwd_chunk, ag_fwd follows gate_fwd, ag_dgrad and ag_wgrad precede
+    gate_bwd, qc_dgrad and qc_wgrad follow coeff_grad_finalize.  (One library
+    kernel can serve several GEMMs, so names alone do not identify them.)"""
     import sqlite3
     c = sqlite3.connect(db)
-    seq = [r[0] for r in c.execute("select kernel_name from counters_collection group by dispatch_id "
-                                   "order by dispatch_id")]
+    seq = [(r[0], r[1]) for r in c.execute("select dispatch_id, kernel_name from counters_collection "
+                                           "group by dispatch_id order by dispatch_id")]
     order = ["gemm_qc_fwd", "gemm_ag_fwd", "gemm_ag_dgrad", "gemm_ag_wgrad", "gemm_qc_dgrad", "gemm_qc_wgrad"]
-    names = {}
-    # walk the last complete fwd+bwd step: from the last gate_bwd back to the agg_fwd before it
-    gb = max(i for i, n in enumerate(seq) if "gate_bwd_kernel" in n)
-    af = max(i for i, n in enumerate(seq[:gb]) if "agg_fwd_chunk" in n)
-    gemms = [n for n in seq[af - 3:] if "Cijk" in n][:6]
-    pre = [n for n in seq[:af] if "Cijk" in n]
-    if pre:
-        gemms = [pre[-1]] + [n for n in seq[af:] if "Cijk" in n][:5]
-    for g, n in zip(order, gemms):
-        names[g] = n[:160]
-    return names
+    gb = max(i for i, (_, n) in enumerate(seq) if "gate_bwd_kernel" in n)
+    af = max(i for i, (_, n) in enumerate(seq[:gb]) if "agg_fwd_chunk" in n)
+    pre = [d for d in seq[:af] if "Cijk" in d[1]]
+    gemms = [pre[-1]] + [d for d in seq[af:] if "Cijk" in d[1]][:5]
+    return {g: (d, n[:160]) for g, (d, n) in zip(order, gemms)}
+
+
+def _pmc_dispatch(db: str, counter: str):
+    """dispatch id -> counter value (summed over instances)."""
+    import sqlite3
+    c = sqlite3.connect(db)
+    return {d: v for d, v in c.execute("select dispatch_id, sum(value) from counters_collection "
+                                       "where counter_name = ? group by dispatch_id", (counter,))}
 
 
 def pmc_summary(cfg_name, dbs):
@@ -395,22 +409,62 @@ def pmc_summary(cfg_name, dbs):
         out["kernels"][name[:160]] = {"fetch_bytes": fb, "write_bytes": wb, "dispatches": fetch[name][0]}
     groups = {}
     for g, names in KERNEL_NAMES.items():
+        # the layer's own kernels: the variant with the most dispatches (the
+        # training step's, not the forward-only pass's) of each named kernel
         tot = 0.0
-        for kname, v in out["kernels"].items():
-            if any(n in kname for n in names):
+        for n in names:
+            cand = [(v["dispatches"], v) for k, v in out["kernels"].items() if n in k]
+            if cand:
+                v = max(cand, key=lambda c: c[0])[1]
                 tot += v["fetch_bytes"] + v["write_bytes"]
         groups[g] = tot
-    gg = _gemm_groups(dbs[0])
-    for g, kname in gg.items():
-        v = out["kernels"].get(kname)
-        if v is not None:
-            groups[g] = v["fetch_bytes"] + v["write_bytes"]
-    out["gemm_kernels"] = gg
+    # projection GEMMs: the dispatches of the last complete step, by order
+    gd = _gemm_dispatches(dbs[0])
+    fd, wd = _pmc_dispatch(dbs[0], "FETCH_SIZE"), _pmc_dispatch(dbs[1], "WRITE_SIZE")
+    for g, (d, _) in gd.items():
+        groups[g] = fd.get(d, 0.0) * 1024.0 * f_scale + wd.get(d, 0.0) * 1024.0 * w_scale
+    out["gemm_kernels"] = {g: n for g, (_, n) in gd.items()}
     out["groups"] = groups
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps({"wrote": path, "groups": groups, "fetch_scale": f_scale, "write_scale": w_scale}))
+
+
+def trace_summary(trace_dir):
+    """Table of a kernel-trace run: calls, average us, share of GPU time, kernel
+    (library GEMMs labelled with their projection from the dispatch order of
+    the last fwd+bwd step)."""
+    import csv
+    stats = list(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_stats.csv"))))
+    trace = sorted(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_trace.csv"))),
+                   key=lambda r: int(r["Dispatch_Id"]))
+    seq = [r["Kernel_Name"] for r in trace]
+    dur = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in trace]
+    order = ["gemm_qc_fwd", "gemm_ag_fwd", "gemm_ag_dgrad", "gemm_ag_wgrad", "gemm_qc_dgrad", "gemm_qc_wgrad"]
+    # every fwd+bwd step: the GEMM before its agg_fwd_chunk, then the five after it
+    per = {g: [] for g in order}
+    label = {}
+    afs = [i for i, n in enumerate(seq) if "agg_fwd_chunk" in n]
+    for k, af in enumerate(afs):
+        end = afs[k + 1] if k + 1 < len(afs) else len(seq)
+        if not any("gate_bwd_kernel" in n for n in seq[af:end]):
+            continue   # a forward-only pass
+        pre = [i for i in range(af) if "Cijk" in seq[i]]
+        idx = [pre[-1]] + [i for i in range(af, end) if "Cijk" in seq[i]][:5]
+        for g, i in zip(order, idx):
+            per[g].append(dur[i])
+            label.setdefault(seq[i], set()).add(g)
+    print("# columns: calls, avg_us, pct_of_gpu_time, kernel (library GEMM names truncated)")
+    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"]
+        tag = f"   [{', '.join(sorted(label[name]))}]" if name in label else ""
+        print(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} {float(r['Percentage']):6.2f}  "
+              f"{name[:100]}{tag}")
+    print("# projection GEMMs of the fwd+bwd steps, labelled by dispatch order: group, calls, avg_us")
+    for g in order:
+        if per[g]:
+            print(f"#   {g:14s} {len(per[g]):4d} {sum(per[g]) / len(per[g]):10.2f}")
 
 
 def traffic_of(cfg_name, group):
@@ -435,6 +489,9 @@ def main():
     if a.pmc_summary:
         pmc_summary(a.config, a.pmc_summary)
         return
+    if a.trace_summary:
+        trace_summary(a.trace_summary)
+        return
     cfg = CONFIGS[a.config]
     ms_step, ms_fwd, per, extra, (dominant, live) = gpu_run(cfg, a.steps, a.warmup,
                                                             not a.no_kernel_timing and not a.graph, a.graph)
@@ -451,6 +508,8 @@ def main():
                          "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
                          "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4),
                          "launches_per_step": len(durs) / a.steps}
+        if name in OVERLAPPED:
+            kernels[name]["overlapped"] = True   # span includes waiting for compute units
     roofline = None
     if kernels and dominant and live:
         k = kernels[dominant]

@@ -10,6 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import weakref
 from typing import Optional
 
 import torch
@@ -178,13 +179,49 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return buf
 
 
+def derived(cache: dict, t: "torch.Tensor", make):
+    """``make(t)``, kept while that same tensor object is alive and unchanged
+    (identity, storage pointer and version counter), so a parameter's derived
+    copy is not rebuilt per call while the parameter does not change.  Keyed
+    by object identity: a freed tensor's address or id reused by a new tensor
+    can never hit a stale copy.  Under stream capture the copy is always
+    rebuilt, so a captured graph recomputes it on every replay (a replay runs
+    no Python and would otherwise keep the capture-time copy)."""
+    if torch.cuda.is_current_stream_capturing():
+        return make(t)
+    hit = cache.get(id(t))
+    if hit is not None:
+        ref, version, ptr, c = hit
+        if ref() is t and version == t._version and ptr == t.data_ptr():
+            return c
+    c = make(t)
+    if len(cache) > 64:
+        for k in [k for k, v in cache.items() if v[0]() is None]:
+            del cache[k]
+        if len(cache) > 64:
+            cache.clear()
+    cache[id(t)] = (weakref.ref(t), t._version, t.data_ptr(), c)
+    return c
+
+
+_table_cache: dict = {}
+
+
+def _f32_table(t: torch.Tensor) -> torch.Tensor:
+    """fp32 contiguous view or cached copy of a RoPE table (a module buffer,
+    bf16 in a bf16 model): converted once per table version, not per call."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t
+    return derived(_table_cache, t, lambda u: u.detach().float().contiguous())
+
+
 class RopeSpec:
     """Device-side RoPE description: fp32 tables and int64 positions kept alive
     for as long as the kernels may read them."""
 
     def __init__(self, kind: int, tables, pos: torch.Tensor):
         self.kind = kind
-        self.tables = [t.float().contiguous() for t in tables]
+        self.tables = [_f32_table(t) for t in tables]
         self.pos = pos.to(torch.int64).contiguous()
         width = self.tables[0].shape[1]
         for t in self.tables:

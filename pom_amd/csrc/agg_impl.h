@@ -419,13 +419,10 @@ static __global__ void __launch_bounds__(kThreads) agg_frame_weights(const AggPa
 // Backward chunk kernel: grad_x for every row of the chunk (written into a
 // strided view, e.g. the h-half of dY) and the chunk's grad_coeff partial.
 // ---------------------------------------------------------------------------
-// Three waves per SIMD: the kernel is memory-bound and latency-limited; the
-// register cap costs at most a few bytes of spill in the plain mode.  With the
-// channel-major copy a lane holds U x CPT2 output values until the staged
-// store, so that variant walks 4 rows per lane instead of 8 to fit the cap.
+// With the channel-major copy a lane holds U x CPT2 output values until the
+// staged store, so that variant walks 4 rows per lane instead of 8.
 template <typename T, int CPT, int KM, int MODE, bool TR>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
-agg_bwd_chunk(const AggParams p) {
+__device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
@@ -624,6 +621,21 @@ agg_bwd_chunk(const AggParams p) {
   }
 }
 
+template <typename T, int CPT, int KM, int MODE, bool TR>
+__global__ void __launch_bounds__(kThreads) agg_bwd_chunk(const AggParams p) {
+  agg_bwd_body<T, CPT, KM, MODE, TR>(p);
+}
+
+// Plain mode at degree <= 2 runs at three waves per SIMD: the kernel is
+// memory-bound and latency-limited, and the register cap costs it at most a
+// few bytes of spill.  Higher degrees and the masked / RoPE modes hold more
+// per-lane state; capped, they spill inside the row loop and run slower.
+template <typename T, int CPT, int KM, int MODE, bool TR>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+agg_bwd_chunk_w3(const AggParams p) {
+  agg_bwd_body<T, CPT, KM, MODE, TR>(p);
+}
+
 // grad_coeff[c, j] = sum over (batch row, chunk) of the partials, fixed order.
 static __global__ void __launch_bounds__(kThreads) coeff_grad_finalize(const float* __restrict__ part, int64_t rows,
                                                                 int64_t P, int K, float* __restrict__ gc) {
@@ -667,7 +679,10 @@ template <typename T, int CPT, int KM, bool TR>
 hipError_t agg_bwd_tr(const AggParams& p, hipStream_t st) {
   const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
   switch (p.mode) {
-    case MODE_PLAIN: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_PLAIN, TR>), grid, block, 0, st, p); break;
+    case MODE_PLAIN:
+      if constexpr (KM <= 2) hipLaunchKernelGGL((agg_bwd_chunk_w3<T, CPT, KM, MODE_PLAIN, TR>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_PLAIN, TR>), grid, block, 0, st, p);
+      break;
     case MODE_MASKED: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_MASKED, TR>), grid, block, 0, st, p); break;
     case MODE_ROPE1D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D, TR>), grid, block, 0, st, p); break;
     case MODE_ROPE2D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D, TR>), grid, block, 0, st, p); break;

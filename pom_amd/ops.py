@@ -20,13 +20,12 @@ from __future__ import annotations
 
 import ctypes
 import os
-import weakref
 from typing import Optional, Tuple
 
 import torch
 
 from . import _lib
-from ._lib import RopeSpec, check, dtype_code, ptr, rope_ptr, view3, workspace, stream_handle
+from ._lib import RopeSpec, check, derived as _derived, dtype_code, ptr, rope_ptr, view3, workspace, stream_handle
 from .gemm_select import tuned_gemms
 
 
@@ -90,31 +89,6 @@ def _check_degree(k: int) -> None:
 
 _f32_cache: dict = {}
 _wt_cache: dict = {}
-
-
-def _derived(cache: dict, t: torch.Tensor, make):
-    """``make(t)``, kept while that same tensor object is alive and unchanged
-    (identity, storage pointer and version counter), so a parameter's derived
-    copy is not rebuilt per call while the parameter does not change.  Keyed
-    by object identity: a freed tensor's address or id reused by a new tensor
-    can never hit a stale copy.  Under stream capture the copy is always
-    rebuilt, so a captured graph recomputes it on every replay (a replay runs
-    no Python and would otherwise keep the capture-time copy)."""
-    if torch.cuda.is_current_stream_capturing():
-        return make(t)
-    hit = cache.get(id(t))
-    if hit is not None:
-        ref, version, ptr, c = hit
-        if ref() is t and version == t._version and ptr == t.data_ptr():
-            return c
-    c = make(t)
-    if len(cache) > 64:
-        for k in [k for k, v in cache.items() if v[0]() is None]:
-            del cache[k]
-        if len(cache) > 64:
-            cache.clear()
-    cache[id(t)] = (weakref.ref(t), t._version, t.data_ptr(), c)
-    return c
 
 
 def _as_f32(t: torch.Tensor) -> torch.Tensor:
@@ -540,8 +514,9 @@ class _PoMLayer(torch.autograd.Function):
             side.wait_stream(cur)
             with torch.cuda.stream(side):
                 gt = transpose(g2, "transpose_g")                  # (D, T), overlaps ag_dgrad
+        wa_k = _weight_t(wa).t() if nt else wa                      # (D, P), K-contiguous when nt
         with _Span("gemm_ag_dgrad"), tuned_gemms():
-            dsh = torch.mm(g2, _weight_t(wa).t()) if nt else torch.mm(g2, wa)   # (T, P)
+            dsh = torch.mm(g2, wa_k)                                # (T, P)
         dw_ag = None
         if need_wa:
             if gt is not None:
@@ -572,8 +547,9 @@ class _PoMLayer(torch.autograd.Function):
                 dyt = transpose(dy, "transpose_dy")                # (2P, T), overlaps qc_dgrad
         dx = None
         if need_x:
+            wq_k = _weight_t(wq).t() if nt else wq                  # (2P, D), K-contiguous when nt
             with _Span("gemm_qc_dgrad"), tuned_gemms():
-                dx = torch.mm(dy, _weight_t(wq).t()) if nt else torch.mm(dy, wq)   # (T, D)
+                dx = torch.mm(dy, wq_k)                             # (T, D)
         dw_qc = None
         if need_wq:
             if want_dyt:
