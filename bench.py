@@ -140,6 +140,9 @@ def kernel_work(cfg, extra):
     if cfg["variant"] == "rope2d":
         rope_tab = 0   # tables are (64, P/4) fp32: cache resident, not counted
     mask_b = B * N * 4 if cfg["variant"] == "masked" else 0
+    # channel-major copies written in the same pass (16-bit training path)
+    from pom_amd import ops
+    cm = T * P * e if (ops._NT_GEMMS and ops._NT_COPIES == "fused") else 0
     w = {
         "gemm_qc_fwd": ("mfma", 2.0 * T * D * 2 * P),
         "gemm_ag_fwd": ("mfma", 2.0 * T * P * D),
@@ -149,12 +152,13 @@ def kernel_work(cfg, extra):
         "gemm_qc_wgrad": ("mfma", 2.0 * T * 2 * P * D),
         # x read (valid tokens only when masked) + aggregate written
         "agg_fwd": ("hbm", float(read_tok * P * e + agg_out + mask_b + rope_tab)),
-        # x read for valid tokens, grad_x written for every token, fp32 upstream grad read
-        "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + B * G * P * 4 + mask_b)),
-        # y_s read, sh written
-        "gate_fwd": ("hbm", float(2 * T * P * e + B * G * P * 4)),
-        # y_s and dsh read, dy_s written
-        "gate_bwd": ("hbm", float(3 * T * P * e + B * G * P * 4)),
+        # x read for valid tokens, grad_x (and its channel-major copy) written for every token,
+        # fp32 upstream grad read
+        "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + cm + B * G * P * 4 + mask_b)),
+        # y_s read, sh (and sh^T) written
+        "gate_fwd": ("hbm", float(2 * T * P * e + cm + B * G * P * 4)),
+        # y_s and dsh read, dy_s (and its channel-major copy) written
+        "gate_bwd": ("hbm", float(3 * T * P * e + cm + B * G * P * 4)),
         # operand-layout transposes for the backward GEMMs: read + write once
         "transpose_x": ("hbm", float(2 * T * D * e)),
         "transpose_sh": ("hbm", float(2 * T * P * e)),
@@ -238,7 +242,7 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
         # copies on the second stream overlap the GEMMs: their event spans
         # include the wait for free compute units, so they are reported but
         # never taken as the dominant kernel
-        dominant = max((k for k in per if k not in OVERLAPPED), key=lambda k: sum(per[k]))
+        dominant = max((k for k in per if k not in overlapped_groups()), key=lambda k: sum(per[k]))
         # the timed region records events around the dominant kernel only
         # (events around every launch would add ~5 % to the step)
         ops.kernel_timer = []
@@ -338,6 +342,11 @@ def cpu_run(cfg, budget_s: float):
 # rocprofv3 kernel names of the launch groups bench.py times
 # launch groups that run on the layer's second stream, concurrently with a GEMM
 OVERLAPPED = {"transpose_x", "transpose_g"}
+
+
+def overlapped_groups():
+    from pom_amd import ops
+    return OVERLAPPED | ({"gemm_ag_wgrad", "gemm_qc_wgrad"} if ops._OVERLAP_GEMMS else set())
 
 KERNEL_NAMES = {
     "agg_fwd": ["agg_fwd_chunk", "agg_fwd_finalize"],
@@ -508,7 +517,7 @@ def main():
                          "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
                          "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4),
                          "launches_per_step": len(durs) / a.steps}
-        if name in OVERLAPPED:
+        if name in overlapped_groups():
             kernels[name]["overlapped"] = True   # span includes waiting for compute units
     roofline = None
     if kernels and dominant and live:

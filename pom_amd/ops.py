@@ -71,6 +71,11 @@ _NT_GEMMS = os.environ.get("POM_AMD_NT_GEMMS", "1") != "0"
 _NT_COPIES = os.environ.get("POM_AMD_NT_COPIES", "fused")
 _copy_streams: dict = {}
 
+# POM_AMD_OVERLAP_GEMMS=1: the weight-gradient GEMMs (off the data-gradient
+# chain) also run on the second stream, concurrently with the gating /
+# aggregation backward and the data-gradient GEMMs.
+_OVERLAP_GEMMS = os.environ.get("POM_AMD_OVERLAP_GEMMS", "0") == "1"
+
 
 def _copy_stream(device: torch.device) -> torch.cuda.Stream:
     idx = device.index if device.index is not None else torch.cuda.current_device()
@@ -518,8 +523,13 @@ class _PoMLayer(torch.autograd.Function):
         with _Span("gemm_ag_dgrad"), tuned_gemms():
             dsh = torch.mm(g2, wa_k)                                # (T, P)
         dw_ag = None
+        over = _OVERLAP_GEMMS and side is not None
         if need_wa:
-            if gt is not None:
+            if gt is not None and over:
+                with torch.cuda.stream(side), _Span("gemm_ag_wgrad"), tuned_gemms():
+                    dw_ag = torch.mm(gt, sht.t())                   # (D, P), on the second stream
+                del gt
+            elif gt is not None:
                 cur.wait_stream(side)
                 gt.record_stream(cur)
                 with _Span("gemm_ag_wgrad"), tuned_gemms():
@@ -545,13 +555,17 @@ class _PoMLayer(torch.autograd.Function):
             side.wait_stream(cur)
             with torch.cuda.stream(side):
                 dyt = transpose(dy, "transpose_dy")                # (2P, T), overlaps qc_dgrad
+        dw_qc = None
+        if need_wq and want_dyt and over:
+            side.wait_stream(cur)                                   # dY^T is complete
+            with torch.cuda.stream(side), _Span("gemm_qc_wgrad"), tuned_gemms():
+                dw_qc = torch.mm(dyt, xt.t())                       # (2P, D), on the second stream
         dx = None
         if need_x:
             wq_k = _weight_t(wq).t() if nt else wq                  # (2P, D), K-contiguous when nt
             with _Span("gemm_qc_dgrad"), tuned_gemms():
                 dx = torch.mm(dy, wq_k)                             # (T, D)
-        dw_qc = None
-        if need_wq:
+        if need_wq and dw_qc is None:
             if want_dyt:
                 if not fused:
                     cur.wait_stream(side)
@@ -563,6 +577,10 @@ class _PoMLayer(torch.autograd.Function):
                     dw_qc = torch.mm(dy.t(), x.reshape(T, D))       # (2P, D)
         if side is not None:
             cur.wait_stream(side)   # join before g2 or dy can be freed
+            if over:
+                for t in (dw_ag, dw_qc):
+                    if t is not None:
+                        t.record_stream(cur)
         g_carry = None
         if has_carry:
             nf = dh.shape[1]
