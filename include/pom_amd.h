@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 3
+#define POM_AMD_ABI_VERSION 4
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -119,9 +119,11 @@ size_t pom_agg_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int K,
                               int64_t frame_len, int rope_kind, int backward);
 
 /* Forward.  out: (B, N/frame_len, P) contiguous in dtype.  count_out: (B,)
- * fp32 sum of the mask weights (masked mode; required there). */
-int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
-                const pom_view* x, const float* coeff,
+ * fp32 sum of the mask weights (masked mode; required there).
+ * coeff: (P, K) contiguous in param_dtype (a pom_dtype; the coefficient
+ * parameter's own type, so no conversion is needed around the call). */
+int pom_agg_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                const pom_view* x, const void* coeff,
                 const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
                 int64_t frame_len, const void* carry, int64_t n_past,
                 const pom_rope* rope,
@@ -132,39 +134,41 @@ int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
  * forward (masked mode).  grad_x: view written for every token (0 where the
  * mask is 0); may alias a slice of a larger buffer (e.g. the h-half of dY).
  * grad_x_t: channel-major copy of grad_x, or NULL (not in token-causal mode).
- * grad_coeff: (P, K) fp32, overwritten.  The gradient of `carry` is
+ * grad_coeff: (P, K) in param_dtype, overwritten.  The gradient of `carry` is
  * n_past * sum_f grad_out[f] / (n_past + f + 1) and is left to the caller. */
-int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K,
-                const pom_view* x, const float* coeff,
+int pom_agg_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                const pom_view* x, const void* coeff,
                 const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
                 const float* count,
                 int64_t frame_len, int64_t n_past,
                 const pom_rope* rope,
                 const float* grad_out, const pom_view* grad_x, const pom_tview* grad_x_t,
-                float* grad_coeff,
+                void* grad_coeff,
                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Gating (pom/pom.py:207, :103-122; query-side RoPE pom/pom_rope.py:522):
  *   sh = R(pos) hardsigmoid(y_s + bias) * hagg[b, n / (N / groups)]
  * hagg: (B, groups, P) contiguous in the element type (the aggregation's
- * output; groups == N gives one row per token).  bias: (P,) fp32 or NULL.
+ * output; groups == N gives one row per token).  bias: (P,) in param_dtype
+ * (the bias parameter's own type) or NULL.
  * ------------------------------------------------------------------------ */
 size_t pom_gate_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t groups,
                                int rope_kind);
 
 /* sh_t: channel-major copy of sh, or NULL. */
-int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P,
-                 const pom_view* ys, const float* bias, const void* hagg, int64_t groups,
+int pom_gate_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P,
+                 const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
                  const pom_rope* rope, const pom_view* sh, const pom_tview* sh_t, void* stream);
 
 /* Backward.  grad_ys: view (e.g. the s-half of dY) receiving dL/dy_s;
  * grad_ys_t: its channel-major copy, or NULL.
- * grad_hagg: (B, groups, P) fp32, 16-byte aligned.  grad_bias: (P,) fp32 or NULL. */
-int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P,
-                 const pom_view* ys, const float* bias, const void* hagg, int64_t groups,
+ * grad_hagg: (B, groups, P) fp32, 16-byte aligned.  grad_bias: (P,) in
+ * param_dtype or NULL. */
+int pom_gate_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P,
+                 const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
                  const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
-                 const pom_tview* grad_ys_t, float* grad_hagg, float* grad_bias,
+                 const pom_tview* grad_ys_t, float* grad_hagg, void* grad_bias,
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------

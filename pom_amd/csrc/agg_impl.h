@@ -259,7 +259,7 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
 #pragma unroll
   for (int i = 0; i < CPT2; ++i)
 #pragma unroll
-    for (int j = 0; j < KM; ++j) c[i][j] = (active && j < p.K) ? p.coeff[map.chan(i) * p.K + j] : 0.0f;
+    for (int j = 0; j < KM; ++j) c[i][j] = (active && j < p.K) ? param_get(p.coeff, map.chan(i) * p.K + j) : 0.0f;
 
   float acc[CPT2];
 #pragma unroll
@@ -448,7 +448,7 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
     const int64_t ch = map.chan(i);
 #pragma unroll
     for (int j = 0; j < KM; ++j) {
-      d[i][j] = (active && j < p.K) ? p.coeff[ch * p.K + j] * (float)(j + 1) : 0.0f;
+      d[i][j] = (active && j < p.K) ? param_get(p.coeff, ch * p.K + j) * (float)(j + 1) : 0.0f;
       g[i][j] = 0.0f;
     }
     float wi = 0.0f;
@@ -638,7 +638,7 @@ agg_bwd_chunk_w3(const AggParams p) {
 
 // grad_coeff[c, j] = sum over (batch row, chunk) of the partials, fixed order.
 static __global__ void __launch_bounds__(kThreads) coeff_grad_finalize(const float* __restrict__ part, int64_t rows,
-                                                                int64_t P, int K, float* __restrict__ gc) {
+                                                                int64_t P, int K, ParamOut gc) {
   const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (idx >= P * K) return;
   const int64_t j = idx / P, c = idx - j * P;
@@ -654,7 +654,7 @@ static __global__ void __launch_bounds__(kThreads) coeff_grad_finalize(const flo
     for (int q = 0; q < 8; ++q) s += v[q];
   }
   for (; r < rows; ++r) s += src[r * stride];
-  gc[c * K + j] = s;
+  param_set(gc, c * K + j, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -202,10 +202,11 @@ hipError_t by_dtype(int dtype, F&& fn) {
 }
 
 // Shared validation and geometry of the aggregation entry points.
-int setup_agg(pom::AggParams& p, int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x,
-              const float* coeff, const float* mask, int64_t msb, int64_t msn, int64_t frame_len,
-              const pom_rope* rope, const pom_view* gx) {
+int setup_agg(pom::AggParams& p, int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+              const pom_view* x, const void* coeff, const float* mask, int64_t msb, int64_t msn,
+              int64_t frame_len, const pom_rope* rope, const pom_view* gx) {
   if (int r = check_dtype(dtype)) return r;
+  if (check_dtype(param_dtype)) return fail(POM_ERR_INVALID, "bad param_dtype %d", param_dtype);
   if (B <= 0 || N <= 0 || P <= 0)
     return fail(POM_ERR_INVALID, "empty shape B=%lld N=%lld P=%lld", (long long)B, (long long)N, (long long)P);
   if (K < 1 || K > POM_MAX_DEGREE) return fail(POM_ERR_UNSUPPORTED, "degree %d outside [1, %d]", K, POM_MAX_DEGREE);
@@ -224,7 +225,7 @@ int setup_agg(pom::AggParams& p, int dtype, int64_t B, int64_t N, int64_t P, int
   }
   p.dtype = dtype; p.K = K; p.B = B; p.N = N; p.P = P;
   p.x = x->data; p.sxb = x->stride_b; p.sxn = x->stride_n;
-  p.coeff = coeff;
+  p.coeff = {coeff, param_dtype};
   p.mask = mask; p.msb = msb; p.msn = msn;
   const void* gxp = gx ? gx->data : nullptr;
   const int64_t sgb = gx ? gx->stride_b : 0, sgn = gx ? gx->stride_n : 0;
@@ -359,12 +360,13 @@ size_t pom_agg_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int K,
   return agg_ws_bytes(B, N, P, K, frame_len, backward != 0);
 }
 
-int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x, const float* coeff,
+int pom_agg_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x,
+                const void* coeff,
                 const float* mask, int64_t mask_stride_b, int64_t mask_stride_n, int64_t frame_len,
                 const void* carry, int64_t n_past, const pom_rope* rope, void* out, float* count_out,
                 void* workspace, size_t workspace_bytes, void* stream) {
   pom::AggParams p;
-  if (int r = setup_agg(p, dtype, B, N, P, K, x, coeff, mask, mask_stride_b, mask_stride_n, frame_len, rope,
+  if (int r = setup_agg(p, dtype, param_dtype, B, N, P, K, x, coeff, mask, mask_stride_b, mask_stride_n, frame_len, rope,
                         nullptr))
     return r;
   if (!out) return fail(POM_ERR_INVALID, "out is null");
@@ -395,14 +397,15 @@ int pom_agg_fwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_vie
                     "pom_agg_fwd launch");
 }
 
-int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x, const float* coeff,
+int pom_agg_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x,
+                const void* coeff,
                 const float* mask, int64_t mask_stride_b, int64_t mask_stride_n, const float* count,
                 int64_t frame_len, int64_t n_past, const pom_rope* rope, const float* grad_out,
-                const pom_view* grad_x, const pom_tview* grad_x_t, float* grad_coeff, void* workspace,
+                const pom_view* grad_x, const pom_tview* grad_x_t, void* grad_coeff, void* workspace,
                 size_t workspace_bytes, void* stream) {
   pom::AggParams p;
   if (int r = check_view(grad_x, "grad_x")) return r;
-  if (int r = setup_agg(p, dtype, B, N, P, K, x, coeff, mask, mask_stride_b, mask_stride_n, frame_len, rope,
+  if (int r = setup_agg(p, dtype, param_dtype, B, N, P, K, x, coeff, mask, mask_stride_b, mask_stride_n, frame_len, rope,
                         grad_x))
     return r;
   if (!grad_out || !grad_coeff) return fail(POM_ERR_INVALID, "grad_out / grad_coeff is null");
@@ -421,7 +424,7 @@ int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_vie
     setup_scan(p, s, sums);
     s.go = grad_out;
     s.gx = grad_x->data; s.sgb = grad_x->stride_b; s.sgn = grad_x->stride_n;
-    s.gc = grad_coeff;
+    s.gc = {grad_coeff, param_dtype};
     s.csum = c.take<float>(B * s.nch * P);
     s.part = c.take<float>(B * s.nch * K * P);
     return hip_status(by_dtype(dtype, [&](auto t) { return pom::scan_bwd_t<decltype(t)>(s, st); }),
@@ -431,7 +434,7 @@ int pom_agg_bwd(int dtype, int64_t B, int64_t N, int64_t P, int K, const pom_vie
   p.go = grad_out;
   p.count_in = count;
   p.gx = grad_x->data; p.sgb = grad_x->stride_b; p.sgn = grad_x->stride_n;
-  p.gc = grad_coeff;
+  p.gc = {grad_coeff, param_dtype};
   p.part = c.take<float>(B * p.g.nch * K * P);
   float* wf = c.take<float>(B * p.g.F * P);
   p.wf = p.g.F > 1 ? wf : nullptr;
@@ -446,24 +449,26 @@ size_t pom_gate_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64
   return gate_ws_bytes(B, N, P, groups);
 }
 
-int pom_gate_fwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys, const float* bias,
-                 const void* hagg, int64_t groups, const pom_rope* rope, const pom_view* sh, const pom_tview* sh_t,
-                 void* stream) {
+int pom_gate_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys,
+                 const void* bias, const void* hagg, int64_t groups, const pom_rope* rope, const pom_view* sh,
+                 const pom_tview* sh_t, void* stream) {
   pom::GateParams p;
   int per_token = 0;
   if (int r = check_view(sh, "sh")) return r;
   if (int r = setup_gate(p, per_token, dtype, B, N, P, ys, hagg, groups, rope, {sh})) return r;
   if (int r = set_tview(p.sht, sh_t, dtype, p.g.cpt, B, N, "sh_t")) return r;
-  p.bias = bias;
+  if (check_dtype(param_dtype)) return fail(POM_ERR_INVALID, "bad param_dtype %d", param_dtype);
+  p.bias = {bias, param_dtype};
   p.sh = sh->data; p.shb = sh->stride_b; p.shn = sh->stride_n;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::gate_fwd_t<decltype(t)>(p, per_token, st); }),
                     "pom_gate_fwd launch");
 }
 
-int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys, const float* bias,
-                 const void* hagg, int64_t groups, const pom_rope* rope, const pom_view* grad_sh,
-                 const pom_view* grad_ys, const pom_tview* grad_ys_t, float* grad_hagg, float* grad_bias,
+int pom_gate_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys,
+                 const void* bias, const void* hagg, int64_t groups, const pom_rope* rope,
+                 const pom_view* grad_sh, const pom_view* grad_ys, const pom_tview* grad_ys_t, float* grad_hagg,
+                 void* grad_bias,
                  void* workspace, size_t workspace_bytes, void* stream) {
   pom::GateParams p;
   int per_token = 0;
@@ -473,11 +478,12 @@ int pom_gate_bwd(int dtype, int64_t B, int64_t N, int64_t P, const pom_view* ys,
   if (!grad_hagg) return fail(POM_ERR_INVALID, "grad_hagg is null");
   if (!aligned(grad_hagg, 4 * p.g.cpt)) return fail(POM_ERR_INVALID, "grad_hagg must be 16-byte aligned");
   if (int r = set_tview(p.dyst, grad_ys_t, dtype, p.g.cpt, B, N, "grad_ys_t")) return r;
-  p.bias = bias;
+  if (check_dtype(param_dtype)) return fail(POM_ERR_INVALID, "bad param_dtype %d", param_dtype);
+  p.bias = {bias, param_dtype};
   p.dsh = grad_sh->data; p.dsb = grad_sh->stride_b; p.dsn = grad_sh->stride_n;
   p.dys = grad_ys->data; p.dyb = grad_ys->stride_b; p.dyn = grad_ys->stride_n;
   p.dhagg = grad_hagg;
-  p.dbias = grad_bias;
+  p.dbias = {grad_bias, param_dtype};
   if (int r = need_ws(workspace, workspace_bytes, gate_ws_bytes(B, N, P, groups))) return r;
   Carve c{static_cast<char*>(workspace), 0};
   p.part_h = c.take<float>(B * p.g.nch * P);

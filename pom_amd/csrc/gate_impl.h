@@ -41,7 +41,7 @@ __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, 
 
   float bias[CPT2], hv[CPT2];
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i) bias[i] = p.bias ? p.bias[map.chan(i)] : 0.0f;
+  for (int i = 0; i < CPT2; ++i) bias[i] = p.bias.ptr ? param_get(p.bias, map.chan(i)) : 0.0f;
   const T* hb = reinterpret_cast<const T*>(p.hagg) + b * ngroups * p.P;
   if (!per_token) {
     Pack<T, CPT> h1, h2;
@@ -154,7 +154,7 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
   const T* hb = reinterpret_cast<const T*>(p.hagg) + b * ngroups * p.P;
 #pragma unroll
   for (int i = 0; i < CPT2; ++i) {
-    bias[i] = (active && p.bias) ? p.bias[map.chan(i)] : 0.0f;
+    bias[i] = (active && p.bias.ptr) ? param_get(p.bias, map.chan(i)) : 0.0f;
     hv[i] = (active && !per_token) ? to_f32<T>(hb[f * p.P + map.chan(i)]) : 0.0f;
     dh[i] = 0.0f;
     db[i] = 0.0f;
@@ -285,7 +285,7 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
   const int nslot = G.lpr * CPT2;
   const int64_t prow = (b * p.g.nch + chunk) * p.P;
   for (int pass = per_token ? 1 : 0; pass < 2; ++pass) {
-    if (pass == 1 && !p.dbias) break;
+    if (pass == 1 && !p.dbias.ptr) break;
     float* dst = pass == 0 ? p.part_h : p.part_b;
 #pragma unroll
     for (int i = 0; i < CPT2; ++i) {
@@ -320,7 +320,7 @@ static __global__ void __launch_bounds__(kThreads) gate_bwd_finalize(const GateP
       p.dhagg[(b * p.g.F + f) * p.P + c] = s;
     }
   }
-  if (p.dbias && idx < p.P) {
+  if (p.dbias.ptr && idx < p.P) {
     const int64_t rows = p.B * nch;
     float s = 0.0f;
     int64_t r = 0;
@@ -332,7 +332,7 @@ static __global__ void __launch_bounds__(kThreads) gate_bwd_finalize(const GateP
       for (int q = 0; q < 8; ++q) s += v[q];
     }
     for (; r < rows; ++r) s += p.part_b[r * p.P + idx];
-    p.dbias[idx] = s;
+    param_set(p.dbias, idx, s);
   }
 }
 

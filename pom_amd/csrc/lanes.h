@@ -13,6 +13,19 @@
 
 namespace pom {
 
+// Parameter element i in fp32 / stored from fp32, in the parameter's dtype.
+__device__ __forceinline__ float param_get(const ParamIn& a, int64_t i) {
+  if (a.dt == DT_BF16) return to_f32<__hip_bfloat16>(static_cast<const __hip_bfloat16*>(a.ptr)[i]);
+  if (a.dt == DT_F16) return to_f32<__half>(static_cast<const __half*>(a.ptr)[i]);
+  return static_cast<const float*>(a.ptr)[i];
+}
+__device__ __forceinline__ void param_set(const ParamOut& a, int64_t i, float v) {
+  if (a.dt == DT_BF16) static_cast<__hip_bfloat16*>(a.ptr)[i] = from_f32<__hip_bfloat16>(v);
+  else if (a.dt == DT_F16) static_cast<__half*>(a.ptr)[i] = from_f32<__half>(v);
+  else static_cast<float*>(a.ptr)[i] = v;
+}
+
+
 // Channel mapping for one lane: slot i in [0, CPT2) -> channel index.
 template <int CPT, int MODE>
 struct LaneMap {

@@ -46,6 +46,18 @@ struct Geom {
   int64_t nch = 1;      // chunks per batch row = F * cpf
 };
 
+// A parameter vector (coefficients, gate bias) or its gradient, in the
+// parameter's own dtype: kernels read and write it directly, so a 16-bit
+// model needs no conversion launches around the layer.
+struct ParamIn {
+  const void* ptr = nullptr;
+  int dt = DT_F32;
+};
+struct ParamOut {
+  void* ptr = nullptr;
+  int dt = DT_F32;
+};
+
 // Optional channel-major ("transposed") copy of a (B, N, P) output:
 // element (b, n, c) at data[c * ld + b * sb + n].  data == nullptr: none.
 struct TrOut {
@@ -62,7 +74,7 @@ struct AggParams {
   int64_t B = 0, N = 0, P = 0;
   const void* x = nullptr;        // (B, N, P) view, unit channel stride
   int64_t sxb = 0, sxn = 0;
-  const float* coeff = nullptr;   // (P, K) fp32
+  ParamIn coeff;                  // (P, K)
 
   const float* mask = nullptr;    // (B, N) weights (masked mode)
   int64_t msb = 0, msn = 0;
@@ -84,7 +96,7 @@ struct AggParams {
   void* gx = nullptr;             // (B, N, P) view, unit channel stride
   int64_t sgb = 0, sgn = 0;
   TrOut gxt;                      // channel-major copy of gx, or none
-  float* gc = nullptr;            // (P, K) fp32
+  ParamOut gc;                    // (P, K)
 
   // workspace
   float* part = nullptr;          // forward (B, nch, P) sums | backward (B, nch, K, P)
@@ -109,14 +121,14 @@ struct ScanParams {
 
   const void* x = nullptr;
   int64_t sxb = 0, sxn = 0;
-  const float* coeff = nullptr;
+  ParamIn coeff;
   RopeTables rope;
 
   void* out = nullptr;            // (B, N, P) element type, contiguous
   const float* go = nullptr;      // (B, N, P) fp32 contiguous upstream gradient
   void* gx = nullptr;
   int64_t sgb = 0, sgn = 0;
-  float* gc = nullptr;
+  ParamOut gc;
 
   float* csum = nullptr;          // (B, nch, P) chunk sums
   float* part = nullptr;          // (B, nch, K, P) backward coefficient partials
@@ -134,7 +146,7 @@ struct GateParams {
   int64_t B = 0, N = 0, P = 0;
   const void* ys = nullptr;       // (B, N, P) gate pre-activation view
   int64_t ysb = 0, ysn = 0;
-  const float* bias = nullptr;    // (P,) fp32 or null
+  ParamIn bias;                   // (P,); ptr null: no bias
   const void* hagg = nullptr;     // (B, G, P) element type
   RopeTables rope;
 
@@ -148,7 +160,7 @@ struct GateParams {
   int64_t dyb = 0, dyn = 0;
   TrOut dyst;                     // channel-major copy of dys, or none
   float* dhagg = nullptr;         // (B, G, P) fp32
-  float* dbias = nullptr;         // (P,) fp32 or null
+  ParamOut dbias;                 // (P,); ptr null: not wanted
 
   float* part_h = nullptr;        // (B, nch, P)
   float* part_b = nullptr;        // (B, nch, P)

@@ -61,7 +61,7 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanParams p) 
 #pragma unroll
   for (int i = 0; i < CPT2; ++i) {
 #pragma unroll
-    for (int j = 0; j < KM; ++j) c[i][j] = j < p.K ? p.coeff[map.chan(i) * p.K + j] : 0.0f;
+    for (int j = 0; j < KM; ++j) c[i][j] = j < p.K ? param_get(p.coeff, map.chan(i) * p.K + j) : 0.0f;
     acc[i] = pre[map.chan(i)];
   }
   const int64_t rbeg = chunk * p.RC;
@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(kThreads) scan_bwd_kernel(const ScanParams p) 
   for (int i = 0; i < CPT2; ++i) {
 #pragma unroll
     for (int j = 0; j < KM; ++j) {
-      c[i][j] = j < p.K ? p.coeff[map.chan(i) * p.K + j] : 0.0f;
+      c[i][j] = j < p.K ? param_get(p.coeff, map.chan(i) * p.K + j) : 0.0f;
       g[i][j] = 0.0f;
     }
     sw[i] = suf[map.chan(i)];

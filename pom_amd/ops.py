@@ -70,6 +70,8 @@ _NT_GEMMS = os.environ.get("POM_AMD_NT_GEMMS", "1") != "0"
 # g^T (inputs of the layer) are always transposed on the second stream.
 _NT_COPIES = os.environ.get("POM_AMD_NT_COPIES", "fused")
 _copy_streams: dict = {}
+# POM_AMD_COPY_STREAM=0: the x^T / g^T transposes run on the current stream.
+_COPY_STREAM = os.environ.get("POM_AMD_COPY_STREAM", "1") != "0"
 
 # POM_AMD_OVERLAP_GEMMS=1: the weight-gradient GEMMs (off the data-gradient
 # chain) also run on the second stream, concurrently with the gating /
@@ -78,6 +80,8 @@ _OVERLAP_GEMMS = os.environ.get("POM_AMD_OVERLAP_GEMMS", "0") == "1"
 
 
 def _copy_stream(device: torch.device) -> torch.cuda.Stream:
+    if not _COPY_STREAM:
+        return torch.cuda.current_stream(device)
     idx = device.index if device.index is not None else torch.cuda.current_device()
     s = _copy_streams.get(idx)
     if s is None:
@@ -96,11 +100,12 @@ _f32_cache: dict = {}
 _wt_cache: dict = {}
 
 
-def _as_f32(t: torch.Tensor) -> torch.Tensor:
-    """fp32 contiguous copy of a small parameter (coefficients, gate bias),
-    cached per parameter version so a bf16 model does not pay a conversion
-    kernel per call."""
-    if t.dtype == torch.float32 and t.is_contiguous():
+def _param(t: torch.Tensor) -> torch.Tensor:
+    """A coefficient / bias parameter as the kernels take it: the tensor itself
+    when it is contiguous fp32, bf16 or fp16 (the kernels read it, and write its
+    gradient, in that dtype), else an fp32 contiguous copy cached per
+    parameter version."""
+    if t.dtype in _lib.DTYPE_CODES and t.is_contiguous():
         return t.detach()
     return _derived(_f32_cache, t, lambda u: u.detach().float().contiguous())
 
@@ -161,17 +166,17 @@ def _weight_t(w: torch.Tensor) -> torch.Tensor:
     return _derived(_wt_cache, w, lambda u: transpose(u.detach(), "transpose_w"))
 
 
-def _coeff32(coeff: torch.Tensor, p: int, k: int) -> torch.Tensor:
+def _coeff_param(coeff: torch.Tensor, p: int, k: int) -> torch.Tensor:
     if coeff.shape != (p, k):
         raise ValueError(f"coeff must have shape ({p}, {k}), got {tuple(coeff.shape)}")
-    return _as_f32(coeff)
+    return _param(coeff)
 
 
 # ---------------------------------------------------------------------------
 # Raw launches (no autograd)
 # ---------------------------------------------------------------------------
 
-def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
+def agg_forward(x: torch.Tensor, coeff: torch.Tensor, k: int, frame_len: int,
                 mask32: Optional[torch.Tensor] = None, carry: Optional[torch.Tensor] = None,
                 n_past: int = 0, rope: Optional[RopeSpec] = None):
     """Launch pom_agg_fwd.  Returns (out (B, N/frame_len, P) x.dtype, count or None)."""
@@ -189,7 +194,7 @@ def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
         if carry.dtype != x.dtype:
             carry = carry.to(x.dtype)
     with _Span("agg_fwd"):
-        rc = lib.pom_agg_fwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+        rc = lib.pom_agg_fwd(dt, dtype_code(coeff), B, N, P, k, ctypes.byref(xv), coeff.data_ptr(), ptr(mask32),
                              mask32.stride(0) if mask32 is not None else 0,
                              mask32.stride(1) if mask32 is not None else 0,
                              frame_len, ptr(carry), n_past, rope_ptr(rope), out.data_ptr(), ptr(count),
@@ -198,18 +203,18 @@ def agg_forward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     return out, count
 
 
-def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int, go32: torch.Tensor,
+def agg_backward(x: torch.Tensor, coeff: torch.Tensor, k: int, frame_len: int, go32: torch.Tensor,
                  grad_x: torch.Tensor, mask32: Optional[torch.Tensor] = None,
                  count: Optional[torch.Tensor] = None, n_past: int = 0,
                  rope: Optional[RopeSpec] = None, grad_x_t: Optional[torch.Tensor] = None,
                  grad_x_rows: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Launch pom_agg_bwd; writes grad_x in place (and, when given, its
     channel-major copy grad_x_t (P, B*N); grad_x_rows is grad_x as (B*N, P))
-    and returns grad_coeff (P, K) fp32."""
+    and returns grad_coeff (P, K) in coeff.dtype."""
     lib = _lib.load()
     B, N, P = x.shape
     dt = dtype_code(x)
-    gc = torch.empty(P, k, dtype=torch.float32, device=x.device)
+    gc = torch.empty(P, k, dtype=coeff.dtype, device=x.device)
     rk = rope.kind if rope is not None else _lib.ROPE_NONE
     nbytes = lib.pom_agg_workspace_size(dt, B, N, P, k, frame_len, rk, 1)
     ws = workspace(x.device, nbytes)
@@ -217,13 +222,19 @@ def agg_backward(x: torch.Tensor, coeff32: torch.Tensor, k: int, frame_len: int,
     go32 = go32.float().contiguous()
     def call(tv):
         with _Span("agg_bwd"):
-            return lib.pom_agg_bwd(dt, B, N, P, k, ctypes.byref(xv), coeff32.data_ptr(), ptr(mask32),
+            return lib.pom_agg_bwd(dt, dtype_code(coeff), B, N, P, k, ctypes.byref(xv), coeff.data_ptr(),
+                                   ptr(mask32),
                                    mask32.stride(0) if mask32 is not None else 0,
                                    mask32.stride(1) if mask32 is not None else 0, ptr(count),
                                    frame_len, n_past, rope_ptr(rope), go32.data_ptr(), ctypes.byref(gv), tv,
                                    gc.data_ptr(), ws.data_ptr(), ws.numel(), stream_handle(x.device))
     _with_copy(call, grad_x_t, grad_x_rows, "transpose_dy", "pom_agg_bwd", B, N)
     return gc
+
+
+def _pdt(t: Optional[torch.Tensor]) -> int:
+    """pom_dtype code of an optional parameter (fp32 when absent)."""
+    return 0 if t is None else dtype_code(t)
 
 
 def _hagg(hagg: torch.Tensor, ys: torch.Tensor) -> torch.Tensor:
@@ -233,7 +244,7 @@ def _hagg(hagg: torch.Tensor, ys: torch.Tensor) -> torch.Tensor:
     return hagg.contiguous()
 
 
-def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.Tensor,
+def gate_forward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor,
                  rope: Optional[RopeSpec] = None, out: Optional[torch.Tensor] = None,
                  out_t: Optional[torch.Tensor] = None) -> torch.Tensor:
     """sh = R hardsigmoid(ys + bias) * hagg[group], via pom_gate_fwd; with
@@ -247,34 +258,37 @@ def gate_forward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.T
 
     def call(tv):
         with _Span("gate_fwd"):
-            return lib.pom_gate_fwd(dtype_code(ys), B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
+            return lib.pom_gate_fwd(dtype_code(ys), _pdt(bias), B, N, P, ctypes.byref(yv), ptr(bias),
+                                    hagg.data_ptr(), G,
                                     rope_ptr(rope), ctypes.byref(sv), tv, stream_handle(ys.device))
     _with_copy(call, out_t, sh.view(B * N, P) if out_t is not None else None, "transpose_sh", "pom_gate_fwd",
                B, N)
     return sh
 
 
-def gate_backward(ys: torch.Tensor, bias32: Optional[torch.Tensor], hagg: torch.Tensor,
+def gate_backward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor,
                   grad_sh: torch.Tensor, grad_ys: torch.Tensor, rope: Optional[RopeSpec] = None,
                   want_bias: bool = True, grad_ys_t: Optional[torch.Tensor] = None,
                   grad_ys_rows: Optional[torch.Tensor] = None):
     """Writes grad_ys in place (and, when given, its channel-major copy
     grad_ys_t (P, B*N); grad_ys_rows is grad_ys as (B*N, P)); returns
-    (grad_hagg (B, G, P) fp32, grad_bias (P,) fp32 or None)."""
+    (grad_hagg (B, G, P) fp32, grad_bias (P,) in bias.dtype or None)."""
     lib = _lib.load()
     B, N, P = ys.shape
     hagg = _hagg(hagg, ys)
     G = hagg.shape[1]
     dt = dtype_code(ys)
     gh = torch.empty(B, G, P, dtype=torch.float32, device=ys.device)
-    gb = torch.empty(P, dtype=torch.float32, device=ys.device) if want_bias else None
+    gb = torch.empty(P, dtype=bias.dtype if bias is not None else torch.float32,
+                     device=ys.device) if want_bias else None
     rk = rope.kind if rope is not None else _lib.ROPE_NONE
     nbytes = lib.pom_gate_workspace_size(dt, B, N, P, G, rk)
     ws = workspace(ys.device, nbytes)
     yv, gv, dv = view3(ys), view3(grad_sh), view3(grad_ys)
     def call(tv):
         with _Span("gate_bwd"):
-            return lib.pom_gate_bwd(dt, B, N, P, ctypes.byref(yv), ptr(bias32), hagg.data_ptr(), G,
+            return lib.pom_gate_bwd(dt, _pdt(bias if bias is not None else gb), B, N, P, ctypes.byref(yv),
+                                    ptr(bias), hagg.data_ptr(), G,
                                     rope_ptr(rope), ctypes.byref(gv), ctypes.byref(dv), tv, gh.data_ptr(),
                                     ptr(gb), ws.data_ptr(), ws.numel(), stream_handle(ys.device))
     _with_copy(call, grad_ys_t, grad_ys_rows, "transpose_dy", "pom_gate_bwd", B, N)
@@ -292,7 +306,7 @@ class _PolyAgg(torch.autograd.Function):
     def forward(ctx, x, coeff, k, frame_len, mask32, rope, carry, n_past):
         _lib.require_device(x)
         B, N, P = x.shape
-        c32 = _coeff32(coeff, P, k)
+        c32 = _coeff_param(coeff, P, k)
         out, count = agg_forward(x, c32, k, frame_len, mask32, carry, n_past, rope)
         ctx.save_for_backward(x, c32, mask32, count)
         ctx.k, ctx.frame_len, ctx.rope, ctx.n_past = k, frame_len, rope, n_past
@@ -387,7 +401,7 @@ class _Gate(torch.autograd.Function):
     def forward(ctx, ys, bias, hagg, rope):
         _lib.require_device(ys, hagg)
         B, N, P = ys.shape
-        b32 = None if bias is None else bias.detach().float().contiguous()
+        b32 = None if bias is None else _param(bias)
         h = _hagg(hagg.detach(), ys)
         sh = gate_forward(ys, b32, h, rope)
         ctx.save_for_backward(ys, b32, h)
@@ -460,9 +474,9 @@ class _PoMLayer(torch.autograd.Function):
             y = torch.mm(x2, wq.t())                                # (T, 2P)
         y3 = y.view(B, N, 2 * P)
         h_view, s_view = y3[..., :P], y3[..., P:]
-        c32 = _coeff32(coeff, P, k)
+        c32 = _coeff_param(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
-        b32 = _as_f32(se_bias)
+        b32 = _param(se_bias)
         fused = want_sht and _NT_COPIES == "fused"
         if fused:
             sht = torch.empty(P, T, dtype=dt, device=dev)

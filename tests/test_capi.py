@@ -73,61 +73,61 @@ def test_validation_errors_before_launch(lib):
     out = ctypes.c_void_p(1024)
     ws = ctypes.c_void_p(4096)
     # empty shape
-    rc = lib.pom_agg_fwd(1, 0, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 0, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID and b"empty shape" in lib.pom_last_error()
     # degree out of range
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 0, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 0, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_UNSUPPORTED
     # frame_len not dividing N
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 5, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 5, None, 0, None, out, None,
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID and b"frame_len" in lib.pom_last_error()
     # null coefficients / output
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), None, None, 0, 0, 16, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), None, None, 0, 0, 16, None, 0, None, out, None,
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, None, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, None, None,
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID
     # workspace missing or too small
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
                          None, 0, None)
     assert rc == _lib.POM_ERR_WORKSPACE
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, None, out, None,
                          ws, 16, None)
     assert rc == _lib.POM_ERR_WORKSPACE
     # masked forward without count_out; masked with frames
     mask = ctypes.c_void_p(2048)
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, mask, 16, 1, 16, None, 0, None, out, None,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, mask, 16, 1, 16, None, 0, None, out, None,
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, mask, 16, 1, 8, None, 0, None, out,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, mask, 16, 1, 8, None, 0, None, out,
                          ctypes.c_void_p(4096), ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_UNSUPPORTED
     # carry with n_past < 1
-    rc = lib.pom_agg_fwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, ctypes.c_void_p(8192), 0,
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, 16, ctypes.c_void_p(8192), 0,
                          None, out, None, ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID
     # RoPE with an odd channel count
     rope = _lib.PomRope(_lib.ROPE_1D, 512, 512, None, None, 32, 16, 0, 512, 1)
-    rc = lib.pom_agg_fwd(1, 2, 16, 63, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, ctypes.byref(rope),
+    rc = lib.pom_agg_fwd(1, 0, 2, 16, 63, 2, ctypes.byref(x), coeff, None, 0, 0, 16, None, 0, ctypes.byref(rope),
                          out, None, ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_INVALID and b"even" in lib.pom_last_error()
     # gate: groups not dividing N
-    rc = lib.pom_gate_fwd(1, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 3, None,
+    rc = lib.pom_gate_fwd(1, 0, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 3, None,
                           ctypes.byref(_view(4096, 1024, 64)), None, None)
     assert rc == _lib.POM_ERR_INVALID
     # channel-major copy: fp32 is not built, overlapping strides are rejected, token-causal has none
     sh = ctypes.byref(_view(4096, 1024, 64))
     tv = ctypes.byref(_lib.PomTView(8192, 32, 16))
-    rc = lib.pom_gate_fwd(0, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 1, None, sh, tv, None)
+    rc = lib.pom_gate_fwd(0, 0, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 1, None, sh, tv, None)
     assert rc == _lib.POM_ERR_UNSUPPORTED and b"16-bit" in lib.pom_last_error()
     bad = ctypes.byref(_lib.PomTView(8192, 20, 16))   # stride_c < (B-1)*stride_b + N
-    rc = lib.pom_gate_fwd(1, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 1, None, sh, bad, None)
+    rc = lib.pom_gate_fwd(1, 0, 2, 16, 64, ctypes.byref(x), None, ctypes.c_void_p(512), 1, None, sh, bad, None)
     assert rc == _lib.POM_ERR_INVALID and b"overlap" in lib.pom_last_error()
-    rc = lib.pom_agg_bwd(1, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, None, 1, 0, None,
+    rc = lib.pom_agg_bwd(1, 0, 2, 16, 64, 2, ctypes.byref(x), coeff, None, 0, 0, None, 1, 0, None,
                          ctypes.c_void_p(2048), ctypes.byref(_view(4096, 1024, 64)), tv, ctypes.c_void_p(1024),
                          ws, 1 << 20, None)
     assert rc == _lib.POM_ERR_UNSUPPORTED and b"token-causal" in lib.pom_last_error()
@@ -194,3 +194,14 @@ def test_transpose_validation_before_launch(lib):
     assert lib.pom_transpose(9, 4, 8, src, 8, dst, 4, None) == _lib.POM_ERR_INVALID   # bad dtype
     assert lib.pom_transpose(1, 4, 8, ctypes.c_void_p(257), 8, dst, 4, None) == _lib.POM_ERR_INVALID
     assert lib.pom_transpose(1, 0, 8, src, 8, dst, 0, None) == _lib.POM_OK            # empty: no launch
+
+
+def test_param_dtype_validation(lib):
+    from pom_amd import _lib
+    x = _view(256, 1024 * 64, 64)
+    rc = lib.pom_agg_fwd(1, 7, 2, 16, 64, 2, ctypes.byref(x), ctypes.c_void_p(512), None, 0, 0, 16, None, 0, None,
+                         ctypes.c_void_p(1024), None, ctypes.c_void_p(4096), 1 << 20, None)
+    assert rc == _lib.POM_ERR_INVALID and b"param_dtype" in lib.pom_last_error()
+    rc = lib.pom_gate_fwd(1, 9, 2, 16, 64, ctypes.byref(x), ctypes.c_void_p(512), ctypes.c_void_p(512), 1, None,
+                          ctypes.byref(_view(4096, 1024, 64)), None, None)
+    assert rc == _lib.POM_ERR_INVALID and b"param_dtype" in lib.pom_last_error()
