@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 4
+#define POM_AMD_ABI_VERSION 5
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -170,6 +170,31 @@ int pom_gate_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P,
                  const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
                  const pom_tview* grad_ys_t, float* grad_hagg, void* grad_bias,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Per-head gating, n_sel_heads = H > 1 (pom/pom.py:118-122 with the gate of
+ * pom/pom.py:207 and the query-side RoPE of pom/pom_rope.py:417-437, :522):
+ *   sh[b, n, c] = R(pos) hardsigmoid(y_s + bias)[b, n, c / (P / H)]
+ *                 * hagg[b, n / (N / groups), c]
+ * y_s: (B, N, H) view; bias: (H,) in param_dtype or NULL.  RoPE acts on the
+ * H gate channels: tables of width >= H/2 (1-D) or >= H/4 (2-D), i.e. the
+ * reference's full-width tables taken every head_dim / 2 (1-D) or head_dim
+ * (2-D) columns.  hagg: (B, groups, P) contiguous in the element type.
+ * ------------------------------------------------------------------------ */
+size_t pom_gate_heads_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t H,
+                                     int64_t groups);
+
+int pom_gate_heads_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
+                       const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
+                       const pom_rope* rope, const pom_view* sh, void* stream);
+
+/* Backward.  grad_ys: (B, N, H) view receiving dL/dy_s.  grad_hagg:
+ * (B, groups, P) fp32.  grad_bias: (H,) in param_dtype or NULL. */
+int pom_gate_heads_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
+                       const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
+                       const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
+                       float* grad_hagg, void* grad_bias,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Operand layout

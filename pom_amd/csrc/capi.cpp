@@ -344,6 +344,79 @@ size_t gate_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t groups) {
   return carve_bytes({B * nc * P, B * nc * P});
 }
 
+// Per-head gating geometry: chunk width V, token-kernel grid, aggregate-
+// gradient chunks.  Depends on the shape only (the workspace size query
+// repeats it without pointers), except V, which also follows alignment.
+struct HeadsGeom {
+  int64_t tok_wgs = 1, RC = 1, cpf = 1, nch = 1, L = 1, G = 1;
+};
+
+HeadsGeom heads_geom(int64_t B, int64_t N, int64_t P, int64_t groups, int V) {
+  HeadsGeom g;
+  const int64_t ntok = B * N;
+  g.tok_wgs = cdiv(ntok, 4);
+  if (g.tok_wgs > 1024) g.tok_wgs = 1024;
+  g.G = groups;
+  g.L = N / groups;
+  const int64_t cols = cdiv(P / V, 256);
+  int64_t cpf = 1;
+  while (B * cols * g.G * cpf < tune().target_wg && cdiv(g.L, 2 * cpf) >= 16) cpf *= 2;
+  g.RC = cdiv(g.L, cpf);
+  g.cpf = cdiv(g.L, g.RC);
+  g.nch = g.G * g.cpf;
+  return g;
+}
+
+size_t heads_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups) {
+  int64_t nch = 1, tok_wgs = 1;
+  for (int V : {1, 2, 4, 8}) {   // every chunk width the call may choose
+    const HeadsGeom g = heads_geom(B, N, P, groups, V);
+    if (g.nch > nch) nch = g.nch;
+    tok_wgs = g.tok_wgs;
+  }
+  return carve_bytes({B * N * H, tok_wgs * H, B * nch * P});
+}
+
+int setup_heads(pom::HeadsParams& p, int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
+                const pom_view* ys, const void* bias, const void* hagg, int64_t groups, const pom_rope* rope,
+                std::initializer_list<const pom_view*> views) {
+  if (int r = check_dtype(dtype)) return r;
+  if (check_dtype(param_dtype)) return fail(POM_ERR_INVALID, "bad param_dtype %d", param_dtype);
+  if (B <= 0 || N <= 0 || P <= 0) return fail(POM_ERR_INVALID, "empty shape");
+  if (H <= 0 || P % H)
+    return fail(POM_ERR_INVALID, "head count %lld must divide P=%lld", (long long)H, (long long)P);
+  if (int r = check_view(ys, "y_s")) return r;
+  for (const pom_view* v : views)
+    if (int r = check_view(v, "gate view")) return r;
+  if (!hagg) return fail(POM_ERR_INVALID, "hagg is null");
+  if (groups <= 0 || N % groups)
+    return fail(POM_ERR_INVALID, "groups %lld must divide N=%lld", (long long)groups, (long long)N);
+  if (int r = check_rope(rope, H, p.rope, p.mode)) return r;
+  p.dtype = dtype; p.B = B; p.N = N; p.P = P; p.H = H; p.hd = P / H;
+  p.ys = ys->data; p.ysb = ys->stride_b; p.ysn = ys->stride_n;
+  p.bias = {bias, param_dtype};
+  p.hagg = hagg;
+  // chunk width: the widest (<= 16 bytes) that divides head_dim and that every
+  // vector operand's base and strides admit
+  const int eb = elem_bytes(dtype);
+  int V = 16 / eb;
+  while (V > 1) {
+    bool ok = p.hd % V == 0 && aligned(hagg, (int64_t)V * eb);
+    for (const pom_view* v : views)
+      ok = ok && aligned(v->data, (int64_t)V * eb) && v->stride_b % V == 0 && v->stride_n % V == 0;
+    if (ok) break;
+    V /= 2;
+  }
+  p.V = V;
+  if (pom::heads_token_smem_bytes(P / V, H) > 64 * 1024)
+    return fail(POM_ERR_UNSUPPORTED, "per-head gating: P/V + 2H = %lld too large for the row kernel",
+                (long long)(P / V + 2 * H));
+  const HeadsGeom g = heads_geom(B, N, P, groups, V);
+  p.tok_wgs = g.tok_wgs; p.RC = g.RC; p.cpf = g.cpf; p.nch = g.nch; p.L = g.L; p.G = g.G;
+  if (p.nch > 65535 || B > 65535) return fail(POM_ERR_UNSUPPORTED, "grid too large");
+  return POM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -491,6 +564,48 @@ int pom_gate_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, co
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::gate_bwd_t<decltype(t)>(p, per_token, st); }),
                     "pom_gate_bwd launch");
+}
+
+size_t pom_gate_heads_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups) {
+  if (check_dtype(dtype) || B <= 0 || N <= 0 || P <= 0 || H <= 0 || P % H || groups <= 0 || N % groups) return 0;
+  return heads_ws_bytes(B, N, P, H, groups);
+}
+
+int pom_gate_heads_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
+                       const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
+                       const pom_rope* rope, const pom_view* sh, void* stream) {
+  pom::HeadsParams p;
+  if (int r = check_view(sh, "sh")) return r;
+  if (int r = setup_heads(p, dtype, param_dtype, B, N, P, H, ys, bias, hagg, groups, rope, {sh})) return r;
+  p.sh = sh->data; p.shb = sh->stride_b; p.shn = sh->stride_n;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return hip_status(by_dtype(dtype, [&](auto t) { return pom::heads_fwd_t<decltype(t)>(p, st); }),
+                    "pom_gate_heads_fwd launch");
+}
+
+int pom_gate_heads_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
+                       const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
+                       const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
+                       float* grad_hagg, void* grad_bias,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  pom::HeadsParams p;
+  if (int r = check_view(grad_sh, "grad_sh")) return r;
+  if (int r = check_view(grad_ys, "grad_ys")) return r;
+  if (int r = setup_heads(p, dtype, param_dtype, B, N, P, H, ys, bias, hagg, groups, rope, {grad_sh})) return r;
+  if (!grad_hagg) return fail(POM_ERR_INVALID, "grad_hagg is null");
+  if (!aligned(grad_hagg, 4)) return fail(POM_ERR_INVALID, "grad_hagg must be 4-byte aligned");
+  p.dsh = grad_sh->data; p.dsb = grad_sh->stride_b; p.dsn = grad_sh->stride_n;
+  p.dys = grad_ys->data; p.dyb = grad_ys->stride_b; p.dyn = grad_ys->stride_n;
+  p.dhagg = grad_hagg;
+  p.dbias = {grad_bias, param_dtype};
+  if (int r = need_ws(workspace, workspace_bytes, heads_ws_bytes(B, N, P, H, groups))) return r;
+  Carve c{static_cast<char*>(workspace), 0};
+  p.sgate = c.take<float>(B * N * H);
+  p.part_b = c.take<float>(p.tok_wgs * H);
+  p.part_h = c.take<float>(B * p.nch * P);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return hip_status(by_dtype(dtype, [&](auto t) { return pom::heads_bwd_t<decltype(t)>(p, st); }),
+                    "pom_gate_heads_bwd launch");
 }
 
 int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src, void* dst,

@@ -2,6 +2,7 @@
 #include "agg_impl.h"
 #include "scan_impl.h"
 #include "gate_impl.h"
+#include "heads_impl.h"
 
 namespace pom {
 template hipError_t agg_fwd_t<__half>(const AggParams&, hipStream_t);
@@ -10,4 +11,6 @@ template hipError_t scan_fwd_t<__half>(const AggParams&, const ScanParams&, hipS
 template hipError_t scan_bwd_t<__half>(const ScanParams&, hipStream_t);
 template hipError_t gate_fwd_t<__half>(const GateParams&, int, hipStream_t);
 template hipError_t gate_bwd_t<__half>(const GateParams&, int, hipStream_t);
+template hipError_t heads_fwd_t<__half>(const HeadsParams&, hipStream_t);
+template hipError_t heads_bwd_t<__half>(const HeadsParams&, hipStream_t);
 }  // namespace pom

@@ -170,6 +170,45 @@ struct GateParams {
 template <typename T> hipError_t gate_fwd_t(const GateParams& p, int per_token, hipStream_t st);
 template <typename T> hipError_t gate_bwd_t(const GateParams& p, int per_token, hipStream_t st);
 
+// Per-head gating (n_sel_heads = H > 1): sh[b,n,c] = rot(hardsigmoid(y_s + bias))[h] * hagg[b, n / L, c],
+// h = c / hd, P = H * hd.
+struct HeadsParams {
+  int dtype = DT_BF16;
+  int mode = MODE_PLAIN;          // PLAIN / ROPE1D / ROPE2D over the H gate channels
+  int V = 1;                      // elements per thread chunk; divides hd
+  int64_t B = 0, N = 0, P = 0, H = 0, hd = 0;
+  int64_t L = 0, G = 1;           // tokens per hagg group, groups (N = G * L)
+
+  const void* ys = nullptr;       // (B, N, H) gate pre-activation view
+  int64_t ysb = 0, ysn = 0;
+  ParamIn bias;                   // (H,); ptr null: no bias
+  const void* hagg = nullptr;     // (B, G, P) element type, contiguous
+  RopeTables rope;                // tables over the H channels: 1-D (S, H/2), 2-D (rows, H/4)
+
+  void* sh = nullptr;             // (B, N, P) output view (forward)
+  int64_t shb = 0, shn = 0;
+
+  const void* dsh = nullptr;      // (B, N, P) upstream gradient view (backward)
+  int64_t dsb = 0, dsn = 0;
+  void* dys = nullptr;            // (B, N, H) gradient of y_s
+  int64_t dyb = 0, dyn = 0;
+  float* dhagg = nullptr;         // (B, G, P) fp32
+  ParamOut dbias;                 // (H,); ptr null: not wanted
+
+  int64_t tok_wgs = 1;            // workgroups of the token-row kernel (= bias partial rows)
+  int64_t RC = 1, cpf = 1, nch = 1;   // aggregate-gradient chunks: cpf chunks of RC rows per group
+  float* sgate = nullptr;         // (B, N, H) fp32 rotated gate values
+  float* part_b = nullptr;        // (tok_wgs, H)
+  float* part_h = nullptr;        // (B, nch, P)
+};
+
+// LDS of the token-row backward kernel: per wave, cpr chunk dots and two
+// H-vectors.
+inline size_t heads_token_smem_bytes(int64_t cpr, int64_t H) { return sizeof(float) * 4 * (size_t)(cpr + 2 * H); }
+
+template <typename T> hipError_t heads_fwd_t(const HeadsParams& p, hipStream_t st);
+template <typename T> hipError_t heads_bwd_t(const HeadsParams& p, hipStream_t st);
+
 // dst (C x R, row stride ldd) = src^T (R x C, row stride lds); elements of elem_bytes (2 or 4).
 hipError_t transpose_t(int elem_bytes, const void* src, int64_t lds, void* dst, int64_t ldd, int64_t R, int64_t C,
                        hipStream_t st);

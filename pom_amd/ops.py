@@ -295,6 +295,55 @@ def gate_backward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Te
     return gh, gb
 
 
+def gate_heads_forward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor, heads: int,
+                       rope: Optional[RopeSpec] = None) -> torch.Tensor:
+    """Per-head gating (n_sel_heads = heads > 1) via pom_gate_heads_fwd:
+    sh[b, n, c] = R hardsigmoid(ys + bias)[b, n, c // (P / heads)] * hagg[b, group(n), c].
+    ys (B, N, heads) view; hagg (B, G, P); rope over the heads gate channels."""
+    lib = _lib.load()
+    B, N, H = ys.shape
+    if H != heads:
+        raise ValueError(f"y_s has {H} channels, expected n_sel_heads = {heads}")
+    hagg = _hagg(hagg, ys)
+    G, P = hagg.shape[1], hagg.shape[2]
+    sh = torch.empty(B, N, P, dtype=ys.dtype, device=ys.device)
+    yv, sv = view3(ys), view3(sh)
+    with _Span("gate_heads_fwd"):
+        rc = lib.pom_gate_heads_fwd(dtype_code(ys), _pdt(bias), B, N, P, H, ctypes.byref(yv), ptr(bias),
+                                    hagg.data_ptr(), G, rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
+    check(rc, "pom_gate_heads_fwd")
+    return sh
+
+
+def gate_heads_backward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor,
+                        grad_sh: torch.Tensor, heads: int, rope: Optional[RopeSpec] = None,
+                        want_bias: bool = True):
+    """Returns (grad_ys (B, N, heads) in ys.dtype, grad_hagg (B, G, P) fp32,
+    grad_bias (heads,) in bias.dtype or None) via pom_gate_heads_bwd."""
+    lib = _lib.load()
+    B, N, H = ys.shape
+    hagg = _hagg(hagg, ys)
+    G, P = hagg.shape[1], hagg.shape[2]
+    if grad_sh.dtype != ys.dtype:
+        grad_sh = grad_sh.to(ys.dtype)
+    if grad_sh.stride(2) != 1:
+        grad_sh = grad_sh.contiguous()
+    dt = dtype_code(ys)
+    gys = torch.empty(B, N, H, dtype=ys.dtype, device=ys.device)
+    gh = torch.empty(B, G, P, dtype=torch.float32, device=ys.device)
+    gb = torch.empty(H, dtype=bias.dtype if bias is not None else torch.float32,
+                     device=ys.device) if want_bias else None
+    ws = workspace(ys.device, lib.pom_gate_heads_workspace_size(dt, B, N, P, H, G))
+    yv, gv, dv = view3(ys), view3(grad_sh), view3(gys)
+    with _Span("gate_heads_bwd"):
+        rc = lib.pom_gate_heads_bwd(dt, _pdt(bias if bias is not None else gb), B, N, P, H, ctypes.byref(yv),
+                                    ptr(bias), hagg.data_ptr(), G, rope_ptr(rope), ctypes.byref(gv),
+                                    ctypes.byref(dv), gh.data_ptr(), ptr(gb), ws.data_ptr(), ws.numel(),
+                                    stream_handle(ys.device))
+    check(rc, "pom_gate_heads_bwd")
+    return gys, gh, gb
+
+
 # ---------------------------------------------------------------------------
 # Kernel-level autograd operators (drop-ins for the Triton entry points)
 # ---------------------------------------------------------------------------
@@ -422,6 +471,34 @@ def gate_hip(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor,
              rope: Optional[RopeSpec] = None) -> torch.Tensor:
     """R(pos) hardsigmoid(ys + bias) * hagg, hagg (B, G, P) broadcast over N/G tokens per group."""
     return _Gate.apply(ys, bias, hagg, rope)
+
+
+class _GateHeads(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ys, bias, hagg, heads, rope):
+        _lib.require_device(ys, hagg)
+        b32 = None if bias is None else _param(bias)
+        h = _hagg(hagg.detach(), ys)
+        sh = gate_heads_forward(ys, b32, h, heads, rope)
+        ctx.save_for_backward(ys, b32, h)
+        ctx.heads, ctx.rope = heads, rope
+        ctx.bias_dtype = None if bias is None else bias.dtype
+        ctx.hagg_dtype = hagg.dtype
+        return sh
+
+    @staticmethod
+    def backward(ctx, grad_sh):
+        ys, b32, h = ctx.saved_tensors
+        gys, gh, gb = gate_heads_backward(ys, b32, h, grad_sh, ctx.heads, ctx.rope, want_bias=b32 is not None)
+        return (gys, None if gb is None else gb.to(ctx.bias_dtype), gh.to(ctx.hagg_dtype), None, None)
+
+
+def gate_heads_hip(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor, heads: int,
+                   rope: Optional[RopeSpec] = None) -> torch.Tensor:
+    """Per-head gate (n_sel_heads = heads > 1): R(pos) hardsigmoid(ys + bias), one
+    scalar per head and token, times hagg (B, G, P) broadcast over N/G tokens
+    per group — pom/pom.py:118-122 with :207 (and pom/pom_rope.py:417-437)."""
+    return _GateHeads.apply(ys, bias, hagg, heads, rope)
 
 
 # ---------------------------------------------------------------------------

@@ -160,27 +160,23 @@ class PoM(nn.Module):
         fl = h.shape[1] if frame_len is None else frame_len
         return ops._PolyAgg.apply(h, self.po_coeff, k, fl, None, rope_h, None, 0)
 
-    def _select(self, ys, bias, h_agg, rope_s=None, rot_s=None):
+    def _select(self, ys, bias, h_agg, rope_s=None):
         """Gate + selection — pom/pom.py:207 and :103-122 (query-side RoPE
-        pom/pom_rope.py:522).  One HIP kernel for n_sel_heads <= 1; per-head
-        scalar gates as tensor ops otherwise."""
+        pom/pom_rope.py:522, :417-437).  One HIP kernel for n_sel_heads <= 1
+        (full-width gate), the per-head kernels for n_sel_heads > 1 (one
+        scalar gate per head and token)."""
         T, G = ys.shape[1], h_agg.shape[1]
         if G not in (1, T) and T % G:
             raise ValueError("query length must be a multiple of the aggregate's group count")
         if self.n_sel_heads > 1:
-            s = F.hardsigmoid(ys + bias)
-            if rot_s is not None:
-                s = rot_s(s)
-            if G not in (1, T):
-                h_agg = h_agg.repeat_interleave(T // G, dim=1)
-            return polynomial_selection_(s, h_agg, self.n_sel_heads)
+            return ops.gate_heads_hip(ys, bias, h_agg, self.n_sel_heads, rope_s)
         return ops.gate_hip(ys, bias, h_agg, rope_s)
 
-    def _mix(self, xq, xc, mask, frame_len, rope_h=None, rope_s=None, rot_h=None, rot_s=None):
+    def _mix(self, xq, xc, mask, frame_len, rope_h=None, rope_s=None, rot_h=None):
         """Unfused route: projections, aggregation, gating, out-projection."""
         h, ys, bias = self._h_and_gate_input(xq, xc)
         h_agg = self._aggregate(h, mask, frame_len, rope_h, rot_h)
-        return self.ag_proj(self._select(ys, bias, h_agg, rope_s, rot_s))
+        return self.ag_proj(self._select(ys, bias, h_agg, rope_s))
 
     def _frame_len(self, mask, n: int) -> Optional[int]:
         if mask is None:

@@ -56,6 +56,10 @@ def apply_rope_2d(x, positions_hw, row_cos, row_sin, col_cos, col_sin):
     return torch.cat([a1 * rc - a2 * rs, a2 * rc + a1 * rs, b1 * cc - b2 * cs, b2 * cc + b1 * cs], dim=-1)
 
 
+# Contiguous per-head gate tables, one per RoPE buffer (and buffer version).
+_HEAD_TABLES: dict = {}
+
+
 class PoMRoPE(PoM):
     """PoM with RoPE after the polynomial and before gating — pom/pom_rope.py:303-526."""
 
@@ -102,6 +106,30 @@ class PoMRoPE(PoM):
             raise ValueError(f"positions must have shape ({n},), got {tuple(positions.shape)}")
         return RopeSpec(_lib.ROPE_1D, [self.freqs_cos, self.freqs_sin], positions.to(device))
 
+    def _spec_heads(self, n: int, positions, positions_hw, device) -> RopeSpec:
+        """Device RoPE description for the n_sel_heads-channel gate: the
+        full-width tables taken every head_dim / 2 (1-D) or head_dim (2-D)
+        columns, as pom/pom_rope.py:417-437 index them, made contiguous once
+        per buffer version."""
+        H = self.n_sel_heads
+        if self.rope_2d:
+            if positions_hw is None:
+                raise ValueError("positions_hw (N, 2) must be provided when rope_2d=True")
+            if positions_hw.shape != (n, 2):
+                raise ValueError(f"positions_hw must have shape ({n}, 2), got {tuple(positions_hw.shape)}")
+            st, q = self.head_dim, H // 4
+            tabs = [_lib.derived(_HEAD_TABLES, t, lambda u: u[:, ::st][:, :q].float().contiguous())
+                    for t in (self.row_cos, self.row_sin, self.col_cos, self.col_sin)]
+            return RopeSpec(_lib.ROPE_2D, tabs, positions_hw.to(device))
+        if positions is None:
+            positions = torch.arange(n, device=device)
+        if positions.shape != (n,):
+            raise ValueError(f"positions must have shape ({n},), got {tuple(positions.shape)}")
+        st, half = self.head_dim // 2, H // 2
+        tabs = [_lib.derived(_HEAD_TABLES, t, lambda u: u[:, ::st][:, :half].float().contiguous())
+                for t in (self.freqs_cos, self.freqs_sin)]
+        return RopeSpec(_lib.ROPE_1D, tabs, positions.to(device))
+
     def _rope_torch(self, x: torch.Tensor, positions, positions_hw) -> torch.Tensor:
         """PoMRoPE._rope — pom/pom_rope.py:386-437 as tensor ops: full-width
         tables for P channels, tables strided by head_dim (2-D) or head_dim / 2
@@ -128,7 +156,7 @@ class PoMRoPE(PoM):
                 ctx_positions_hw: Optional[torch.Tensor] = None) -> torch.Tensor:
         """pom/pom_rope.py:443-526.  Context features are rotated before they are
         aggregated (inside the aggregation kernel), the query gate after the
-        hardsigmoid (inside the gating kernel, or as tensor ops for
+        hardsigmoid (inside the gating kernel; the per-head kernels for
         n_sel_heads > 1)."""
         self_mixing = xc is None or xc is xq
         if xc is None:
@@ -138,7 +166,6 @@ class PoMRoPE(PoM):
         eff_ctx_hw = ctx_positions_hw if ctx_positions_hw is not None else (positions_hw if self_mixing else None)
         rope_h = self._spec(xc.shape[1], eff_ctx, eff_ctx_hw, xc.device)
         rot_h = lambda t: self._rope_torch(t, eff_ctx, eff_ctx_hw)
-        rot_s = lambda t: self._rope_torch(t, positions, positions_hw)
         fl = self._frame_len(mask, xc.shape[1])
         if self._fused_ok(xq, xc) and (mask is None or fl is not None):
             rope_s = self._spec(xq.shape[1], positions, positions_hw, xq.device)
@@ -146,5 +173,8 @@ class PoMRoPE(PoM):
                                    self.ag_proj.weight, self.ag_proj.bias, self.order, fl, None,
                                    rope_h, rope_s)
             return out
-        rope_s = None if self.n_sel_heads > 1 else self._spec(xq.shape[1], positions, positions_hw, xq.device)
-        return self._mix(xq, xc, mask, fl, rope_h, rope_s, rot_h, rot_s)
+        if self.n_sel_heads > 1:
+            rope_s = self._spec_heads(xq.shape[1], positions, positions_hw, xq.device)
+        else:
+            rope_s = self._spec(xq.shape[1], positions, positions_hw, xq.device)
+        return self._mix(xq, xc, mask, fl, rope_h, rope_s, rot_h)

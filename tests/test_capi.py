@@ -32,7 +32,8 @@ def lib():
 def test_header_lists_expected_entry_points():
     names = _declared_functions()
     for n in ["pom_abi_version", "pom_last_error", "pom_agg_workspace_size", "pom_agg_fwd", "pom_agg_bwd",
-              "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd", "pom_transpose"]:
+              "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd", "pom_gate_heads_workspace_size",
+              "pom_gate_heads_fwd", "pom_gate_heads_bwd", "pom_transpose"]:
         assert n in names
 
 
@@ -205,3 +206,36 @@ def test_param_dtype_validation(lib):
     rc = lib.pom_gate_fwd(1, 9, 2, 16, 64, ctypes.byref(x), ctypes.c_void_p(512), ctypes.c_void_p(512), 1, None,
                           ctypes.byref(_view(4096, 1024, 64)), None, None)
     assert rc == _lib.POM_ERR_INVALID and b"param_dtype" in lib.pom_last_error()
+
+
+def test_heads_validation_before_launch(lib):
+    """Per-head gating rejects bad shapes and RoPE layouts before any launch."""
+    from pom_amd import _lib
+    ys = ctypes.byref(_view(256, 64 * 8, 8))
+    sh = ctypes.byref(_view(4096, 64 * 64, 64))
+    hagg = ctypes.c_void_p(8192)
+    # H must divide P
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 7, ys, None, hagg, 1, None, sh, None)
+    assert rc == _lib.POM_ERR_INVALID and b"divide P" in lib.pom_last_error()
+    # groups must divide N
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 5, None, sh, None)
+    assert rc == _lib.POM_ERR_INVALID and b"groups" in lib.pom_last_error()
+    # 1-D RoPE needs an even head count, 2-D a multiple of 4, tables wide enough
+    pos = ctypes.c_void_p(512)
+    r1 = _lib.PomRope(_lib.ROPE_1D, 1024, 2048, None, None, 4, 16, 0, pos.value, 1)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 63, 7, ys, None, hagg, 1, ctypes.byref(r1), sh, None)
+    assert rc == _lib.POM_ERR_INVALID and b"even" in lib.pom_last_error()
+    r1n = _lib.PomRope(_lib.ROPE_1D, 1024, 2048, None, None, 3, 16, 0, pos.value, 1)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 1, ctypes.byref(r1n), sh, None)
+    assert rc == _lib.POM_ERR_INVALID and b"narrower" in lib.pom_last_error()
+    r2 = _lib.PomRope(_lib.ROPE_2D, 1024, 2048, 1024, 2048, 2, 16, 16, pos.value, 2)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 60, 6, ys, None, hagg, 1, ctypes.byref(r2), sh, None)
+    assert rc == _lib.POM_ERR_INVALID and b"divisible by 4" in lib.pom_last_error()
+    # parameter dtype and a short workspace
+    rc = lib.pom_gate_heads_fwd(1, 9, 2, 64, 64, 8, ys, None, hagg, 1, None, sh, None)
+    assert rc == _lib.POM_ERR_INVALID and b"param_dtype" in lib.pom_last_error()
+    need = lib.pom_gate_heads_workspace_size(1, 2, 64, 64, 8, 1)
+    assert need > 0 and lib.pom_gate_heads_workspace_size(1, 2, 64, 64, 7, 1) == 0
+    rc = lib.pom_gate_heads_bwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 1, None, sh, ys, ctypes.c_void_p(1 << 16),
+                                None, ctypes.c_void_p(1 << 20), need - 1, None)
+    assert rc == _lib.POM_ERR_WORKSPACE
