@@ -61,7 +61,7 @@ __device__ __forceinline__ void chunk_rows(const Geom& g, int64_t chunk, int64_t
 
 template <int MODE>
 struct Mode_ {
-  static constexpr bool rope = (MODE == MODE_ROPE1D || MODE == MODE_ROPE2D);
+  static constexpr bool rope = (mode_layout(MODE) == MODE_ROPE1D || mode_layout(MODE) == MODE_ROPE2D);
   static constexpr int U = rope ? 4 : 8;   // rows in flight per lane
 };
 
@@ -235,7 +235,7 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
-  constexpr bool MASKED = MODE == MODE_MASKED;
+  constexpr bool MASKED = mode_masked(MODE);
   constexpr int U = Mode_<MODE>::U;
   __shared__ float red[kWaves][kMaxLpr * CPT2];
 
@@ -297,12 +297,16 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
           float h1 = act(v1[u].get(i)), h2 = act(v2[u].get(i));
-          if (TAIL) {
+          if (TAIL || MASKED) {
             h1 = keep ? h1 : 0.0f;
             h2 = keep ? h2 : 0.0f;
           }
-          const float p1 = poly<KM>(h1, c[i]);
-          const float p2 = poly<KM>(h2, c[CPT + i]);
+          float p1 = poly<KM>(h1, c[i]);
+          float p2 = poly<KM>(h2, c[CPT + i]);
+          if constexpr (MASKED) {   // the mask weights the rotated features
+            p1 *= wv[u];
+            p2 *= wv[u];
+          }
           acc[i] += p1 * cs[i] - p2 * sn[i];
           acc[CPT + i] += p2 * cs[i] + p1 * sn[i];
         }
@@ -426,7 +430,7 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
-  constexpr bool MASKED = MODE == MODE_MASKED;
+  constexpr bool MASKED = mode_masked(MODE);
   constexpr int U = TR && !ROPE ? 4 : Mode_<MODE>::U;
   __shared__ float red[kWaves][kMaxLpr * CPT2];
 
@@ -481,12 +485,16 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
       float z[CPT];
 #pragma unroll
       for (int i = 0; i < CPT; ++i) z[i] = 0.0f;
-      for (int64_t n = rbeg + G.wave * G.rpw + G.lrow; n < first; n += G.rs)
+      for (int64_t n = rbeg + G.wave * G.rpw + G.lrow; n < first; n += G.rs) {
         VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
-      for (int64_t n = last + G.wave * G.rpw + G.lrow; n < rend; n += G.rs)
+        if constexpr (ROPE) VecIO<T, CPT>::store(gxb + n * p.sgn + map.c2, z);
+      }
+      for (int64_t n = last + G.wave * G.rpw + G.lrow; n < rend; n += G.rs) {
         VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
+        if constexpr (ROPE) VecIO<T, CPT>::store(gxb + n * p.sgn + map.c2, z);
+      }
     }
-    if constexpr (TR) {
+    if constexpr (TR && !ROPE) {
       const int64_t c0 = slab * G.lpr * CPT;
       const int64_t nc = p.P - c0 < G.lpr * CPT ? p.P - c0 : G.lpr * CPT;
       zero_tr<T>(p.gxt, b, rbeg, first, c0, nc);
@@ -529,17 +537,27 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
       if constexpr (ROPE) {
         float cs[CPT], sn[CPT];
         load_table<CPT>(p.rope, map.table, n, map.tcol, cs, sn);
+        bool keep = in;
+        float mw = 1.0f;
+        if constexpr (MASKED) {
+          keep = keep && mv[u] != 0.0f;
+          mw = mv[u];
+        }
 #pragma unroll
-        for (int i = 0; i < CPT; ++i) {   // R^T applied to (w1, w2)
-          const float wa = w[i] * cs[i] + w[CPT + i] * sn[i];
-          const float wb = w[CPT + i] * cs[i] - w[i] * sn[i];
+        for (int i = 0; i < CPT; ++i) {   // R^T applied to (w1, w2), times the token's mask weight
+          const float wa = (w[i] * cs[i] + w[CPT + i] * sn[i]) * mw;
+          const float wb = (w[CPT + i] * cs[i] - w[i] * sn[i]) * mw;
           const float x1 = v1[u].get(i), x2 = v2[u].get(i);
           const float l1 = leaky(x1), l2 = leaky(x2);
           const float h1 = clamp_act(l1), h2 = clamp_act(l2);
           gv1[i] = weighted_act_grad(x1, l1, h1, wa, 0.01f * wa) * poly_d<KM>(h1, d[i]);
           gv2[i] = weighted_act_grad(x2, l2, h2, wb, 0.01f * wb) * poly_d<KM>(h2, d[CPT + i]);
-          pow_acc<KM>(in ? h1 : 0.0f, wa, g[i]);
-          pow_acc<KM>(in ? h2 : 0.0f, wb, g[CPT + i]);
+          if constexpr (MASKED) {   // padded token: zero gradient
+            gv1[i] = keep ? gv1[i] : 0.0f;
+            gv2[i] = keep ? gv2[i] : 0.0f;
+          }
+          pow_acc<KM>(keep ? h1 : 0.0f, wa, g[i]);
+          pow_acc<KM>(keep ? h2 : 0.0f, wb, g[CPT + i]);
         }
         if (active && in) {
           VecIO<T, CPT>::store(grow + map.c1, gv1);
@@ -670,6 +688,12 @@ hipError_t agg_fwd_mode(const AggParams& p, hipStream_t st) {
     case MODE_MASKED: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_MASKED>), grid, block, 0, st, p); break;
     case MODE_ROPE1D: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_ROPE1D>), grid, block, 0, st, p); break;
     case MODE_ROPE2D: hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_ROPE2D>), grid, block, 0, st, p); break;
+    case MODE_ROPE1D_MASKED:
+      hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_ROPE1D_MASKED>), grid, block, 0, st, p);
+      break;
+    case MODE_ROPE2D_MASKED:
+      hipLaunchKernelGGL((agg_fwd_chunk<T, CPT, KM, MODE_ROPE2D_MASKED>), grid, block, 0, st, p);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -686,6 +710,15 @@ hipError_t agg_bwd_tr(const AggParams& p, hipStream_t st) {
     case MODE_MASKED: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_MASKED, TR>), grid, block, 0, st, p); break;
     case MODE_ROPE1D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D, TR>), grid, block, 0, st, p); break;
     case MODE_ROPE2D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D, TR>), grid, block, 0, st, p); break;
+    // masked RoPE: no channel-major copy (the C ABI rejects the request)
+    case MODE_ROPE1D_MASKED:
+      if constexpr (TR) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D_MASKED, false>), grid, block, 0, st, p);
+      break;
+    case MODE_ROPE2D_MASKED:
+      if constexpr (TR) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D_MASKED, false>), grid, block, 0, st, p);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -753,7 +786,7 @@ template <typename T>
 hipError_t agg_fwd_t(const AggParams& p, hipStream_t st) {
   hipError_t e = agg_fwd_chunks<T>(p, st);
   if (e != hipSuccess || p.direct) return e;
-  if (p.mode == MODE_MASKED)
+  if (mode_masked(p.mode))
     hipLaunchKernelGGL((agg_fwd_finalize<T, true>), flat_grid(p.B * p.P), dim3(kThreads), 0, st, p);
   else
     hipLaunchKernelGGL((agg_fwd_finalize<T, false>), flat_grid(p.B * p.P), dim3(kThreads), 0, st, p);

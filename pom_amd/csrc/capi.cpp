@@ -184,12 +184,12 @@ int check_rope(const pom_rope* r, int64_t P, pom::RopeTables& t, int& mode) {
   return POM_OK;
 }
 
-bool is_rope(int mode) { return mode == pom::MODE_ROPE1D || mode == pom::MODE_ROPE2D; }
+bool is_rope(int mode) {
+  return pom::mode_layout(mode) == pom::MODE_ROPE1D || pom::mode_layout(mode) == pom::MODE_ROPE2D;
+}
 
 // Units (channels or rotation pairs) a lane vector covers.
-int64_t unit_count(int mode, int64_t P) {
-  return mode == pom::MODE_ROPE2D || mode == pom::MODE_ROPE1D ? P / 2 : P;
-}
+int64_t unit_count(int mode, int64_t P) { return is_rope(mode) ? P / 2 : P; }
 
 template <typename F>
 hipError_t by_dtype(int dtype, F&& fn) {
@@ -217,9 +217,9 @@ int setup_agg(pom::AggParams& p, int dtype, int param_dtype, int64_t B, int64_t 
   int rmode;
   if (int r = check_rope(rope, P, p.rope, rmode)) return r;
   if (mask) {
-    if (rmode != pom::MODE_PLAIN) return fail(POM_ERR_UNSUPPORTED, "masked aggregation with RoPE");
     if (frame_len != N) return fail(POM_ERR_UNSUPPORTED, "masked aggregation with frames");
-    p.mode = pom::MODE_MASKED;
+    p.mode = rmode == pom::MODE_ROPE1D ? pom::MODE_ROPE1D_MASKED
+           : rmode == pom::MODE_ROPE2D ? pom::MODE_ROPE2D_MASKED : pom::MODE_MASKED;
   } else {
     p.mode = rmode;
   }
@@ -230,7 +230,7 @@ int setup_agg(pom::AggParams& p, int dtype, int param_dtype, int64_t B, int64_t 
   const void* gxp = gx ? gx->data : nullptr;
   const int64_t sgb = gx ? gx->stride_b : 0, sgn = gx ? gx->stride_n : 0;
   const int64_t units = unit_count(p.mode, P);
-  p.g.cpt = choose_cpt(dtype, p.mode == pom::MODE_ROPE2D ? P / 4 : units, {x->data, gxp},
+  p.g.cpt = choose_cpt(dtype, pom::mode_layout(p.mode) == pom::MODE_ROPE2D ? P / 4 : units, {x->data, gxp},
                        {x->stride_b, x->stride_n, sgb, sgn}, is_rope(p.mode) ? &p.rope : nullptr);
   p.g.nvec = units / p.g.cpt;
   choose_slabs(p.g);
@@ -487,6 +487,8 @@ int pom_agg_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int
   if (n_past > 0 && frame_len == 1 && N > 1) return fail(POM_ERR_UNSUPPORTED, "carry with token-causal aggregation");
   if (grad_x_t && frame_len == 1 && N > 1)
     return fail(POM_ERR_UNSUPPORTED, "grad_x_t with token-causal aggregation");
+  if (grad_x_t && mask && is_rope(p.mode))
+    return fail(POM_ERR_UNSUPPORTED, "grad_x_t with masked RoPE aggregation");
   if (int r = set_tview(p.gxt, grad_x_t, dtype, p.g.cpt, B, N, "grad_x_t")) return r;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (int r = need_ws(workspace, workspace_bytes, agg_ws_bytes(B, N, P, K, frame_len, true))) return r;

@@ -29,15 +29,16 @@ __device__ __forceinline__ void param_set(const ParamOut& a, int64_t i, float v)
 // Channel mapping for one lane: slot i in [0, CPT2) -> channel index.
 template <int CPT, int MODE>
 struct LaneMap {
-  static constexpr int CPT2 = (MODE == MODE_ROPE1D || MODE == MODE_ROPE2D) ? 2 * CPT : CPT;
+  static constexpr int LAY = mode_layout(MODE);
+  static constexpr int CPT2 = (LAY == MODE_ROPE1D || LAY == MODE_ROPE2D) ? 2 * CPT : CPT;
   int64_t c1 = 0, c2 = 0, tcol = 0;
   int table = 0;   // 0 = row / 1-D tables, 1 = column tables (2-D)
 
   __device__ __forceinline__ void init(int64_t vcol, int64_t P) {
-    if constexpr (MODE == MODE_ROPE1D) {
+    if constexpr (LAY == MODE_ROPE1D) {
       const int64_t j = vcol * CPT;
       c1 = j; c2 = j + P / 2; tcol = j;
-    } else if constexpr (MODE == MODE_ROPE2D) {
+    } else if constexpr (LAY == MODE_ROPE2D) {
       const int64_t q = P / 4, j = vcol * CPT;
       if (j < q) { c1 = j; c2 = j + q; tcol = j; table = 0; }
       else { const int64_t jj = j - q; c1 = 2 * q + jj; c2 = 3 * q + jj; tcol = jj; table = 1; }

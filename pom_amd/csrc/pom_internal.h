@@ -9,7 +9,19 @@ namespace pom {
 
 enum DType { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
-enum Mode { MODE_PLAIN = 0, MODE_MASKED = 1, MODE_ROPE1D = 2, MODE_ROPE2D = 3 };
+enum Mode {
+  MODE_PLAIN = 0, MODE_MASKED = 1, MODE_ROPE1D = 2, MODE_ROPE2D = 3,
+  MODE_ROPE1D_MASKED = 4, MODE_ROPE2D_MASKED = 5   // RoPE with (B, N) mask weights (aggregation only)
+};
+
+// Channel layout of a mode (PLAIN, ROPE1D or ROPE2D) and whether it weights
+// tokens by a mask.
+__host__ __device__ constexpr int mode_layout(int m) {
+  return m == MODE_MASKED ? MODE_PLAIN : m == MODE_ROPE1D_MASKED ? MODE_ROPE1D : m == MODE_ROPE2D_MASKED ? MODE_ROPE2D : m;
+}
+__host__ __device__ constexpr bool mode_masked(int m) {
+  return m == MODE_MASKED || m == MODE_ROPE1D_MASKED || m == MODE_ROPE2D_MASKED;
+}
 
 // RoPE cos/sin tables (fp32, row stride `stride`) and integer positions.
 // 1-D: table 0 = (S, P/2), pos[n * pos_sn].

@@ -6,11 +6,9 @@ reductions, run as GPU library operations (no CPU path).
   as one batched GEMM on the matrix cores, divided by the mask's row sums.
   This is O(M * N * P) by nature; frame-causal video masks should use the
   O(N) ``block_causal(frame_len)`` descriptor instead.
-* RoPE combined with a (B, N) key-padding mask (pom/pom_rope.py:511-515):
-  features, rotation and the masked mean as GPU tensor operations.
 
-Both follow the reference's operation order (pom/pom.py:83-99,
-pom/pom_rope.py:242-296) so autograd gives the reference's gradients.
+It follows the reference's operation order (pom/pom.py:83-99) so autograd
+gives the reference's gradients.
 """
 from __future__ import annotations
 
@@ -39,12 +37,3 @@ def full_mask_mix(h: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
         raise ValueError(f"mask must have shape (B, M, N) = ({h.shape[0]}, M, {h.shape[1]}), got {tuple(m.shape)}")
     out = torch.bmm(m.contiguous(), h.contiguous())
     return out / m.sum(dim=2, keepdim=True)
-
-
-def masked_mean(h: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-    """(B, N, P), (B, N) -> (B, 1, P) — pom/pom.py:35-38 with the GPU kernels'
-    convention that an all-masked row aggregates to 0."""
-    m = mask.to(device=h.device, dtype=h.dtype).unsqueeze(-1)
-    num = (h * m).sum(dim=1, keepdim=True)
-    den = m.sum(dim=1, keepdim=True)
-    return torch.where(den != 0, num / torch.where(den != 0, den, torch.ones_like(den)), torch.zeros_like(num))

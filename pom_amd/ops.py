@@ -390,10 +390,12 @@ def poly_agg_mean_hip(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Ten
     return _PolyAgg.apply(x, coeff, k, x.shape[1], None, None, None, 0)
 
 
-def poly_agg_masked_hip(x: torch.Tensor, mask: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
-    """(B, N, D), (B, N) weights -> (B, 1, D) weighted mean (all-zero row -> 0)."""
+def poly_agg_masked_hip(x: torch.Tensor, mask: torch.Tensor, coeff: torch.Tensor, k: int,
+                        rope: Optional[RopeSpec] = None) -> torch.Tensor:
+    """(B, N, D), (B, N) weights -> (B, 1, D) weighted mean (all-zero row -> 0);
+    with rope, of the rotated features (pom/pom_rope.py:511-515)."""
     _check_degree(k)
-    return _PolyAgg.apply(x, coeff, k, x.shape[1], _mask32(mask, x), None, None, 0)
+    return _PolyAgg.apply(x, coeff, k, x.shape[1], _mask32(mask, x), rope, None, 0)
 
 
 def poly_agg_block_causal_hip(x: torch.Tensor, coeff: torch.Tensor, k: int, frame_len: int) -> torch.Tensor:

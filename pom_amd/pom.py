@@ -154,9 +154,7 @@ class PoM(nn.Module):
             p = dense.poly_features(h, self.po_coeff, k)
             return dense.full_mask_mix(rot_h(p) if rot_h is not None else p, mask)
         if isinstance(mask, torch.Tensor) and mask.dim() == 2:
-            if rope_h is not None:
-                return dense.masked_mean(rot_h(dense.poly_features(h, self.po_coeff, k)), mask)
-            return ops.poly_agg_masked_hip(h, mask, self.po_coeff, k)
+            return ops.poly_agg_masked_hip(h, mask, self.po_coeff, k, rope_h)
         fl = h.shape[1] if frame_len is None else frame_len
         return ops._PolyAgg.apply(h, self.po_coeff, k, fl, None, rope_h, None, 0)
 

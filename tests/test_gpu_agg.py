@@ -71,7 +71,9 @@ def run_case(device, B, N, D, K, dtype, kind, strided=False, frame_len=None, kee
     else:
         xd_leaf = xd
         xin = xd
-    if rope is not None:
+    if rope is not None and kind == "masked":
+        got = ops.poly_agg_masked_hip(xin, mask.to(device), cd, K, rope["spec"](device))
+    elif rope is not None:
         spec = rope["spec"](device)
         fl = N if kind == "mean" else (1 if kind == "causal" else frame_len)
         got = ops.poly_agg_rope_hip(xin, cd, K, spec, fl)
@@ -219,6 +221,47 @@ def test_rope1d_causal(device, B, N, D, K, dtype):
 @pytest.mark.parametrize("B,H,W,D,K", [(2, 8, 8, 64, 2), (1, 16, 16, 96, 3), (2, 32, 32, 384, 2)])
 def test_rope2d_mean(device, B, H, W, D, K, dtype):
     run_case(device, B, H * W, D, K, dtype, "mean", rope=_rope2d(D, H, W), strided=True)
+
+
+@pytest.mark.parametrize("keep", [0.5, 0.25])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,N,D,K", [(2, 64, 64, 2), (3, 256, 96, 3), (2, 1024, 128, 2), (1, 33, 32, 16)])
+def test_rope1d_masked(device, B, N, D, K, dtype, keep):
+    """RoPE with a (B, N) padding mask: masked mean of the rotated features
+    (pom/pom_rope.py:511-515)."""
+    run_case(device, B, N, D, K, dtype, "masked", keep=keep, rope=_rope1d(D, N, random_pos=True),
+             strided=dtype != torch.float32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,W,D,K", [(2, 8, 8, 64, 2), (2, 16, 16, 96, 3)])
+def test_rope2d_masked(device, B, H, W, D, K, dtype):
+    run_case(device, B, H * W, D, K, dtype, "masked", keep=0.5, rope=_rope2d(D, H, W), strided=True)
+
+
+def test_rope_masked_invariants(device):
+    """Masked RoPE: an all-ones mask gives the RoPE mean, an all-zero row gives
+    0, padded tokens (even huge ones) never change the output or get a
+    gradient."""
+    B, N, D, K = 3, 256, 64, 2
+    _, x, c = make_inputs(B, N, D, K, torch.float32)
+    r = _rope1d(D, N, random_pos=True)
+    spec = r["spec"](device)
+    xd, cd = x.to(device), c.to(device)
+    ones = torch.ones(B, N, device=device)
+    a = ops.poly_agg_masked_hip(xd, ones, cd, K, spec)
+    b = ops.poly_agg_rope_hip(xd, cd, K, spec, N)
+    assert (a - b).abs().max().item() <= 1e-6
+    m = (torch.arange(N).view(1, N) < torch.tensor([100, 256, 0]).view(B, 1)).float().to(device)
+    x2 = x.clone()
+    x2[(m == 0).cpu()] = torch.randn(int((m == 0).sum()), D) * 50
+    x2d = x2.to(device).requires_grad_(True)
+    o1 = ops.poly_agg_masked_hip(xd, m, cd, K, spec)
+    o2 = ops.poly_agg_masked_hip(x2d, m, cd, K, spec)
+    assert torch.equal(o1, o2)
+    assert torch.all(o2[2] == 0) and torch.isfinite(o2).all()
+    o2.sum().backward()
+    assert torch.all(x2d.grad[m == 0] == 0)
 
 
 def test_state_carry_matches_frames(device):
