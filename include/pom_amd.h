@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 5
+#define POM_AMD_ABI_VERSION 6
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -195,6 +195,25 @@ int pom_gate_heads_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t
                        const pom_rope* rope, const pom_view* grad_sh, const pom_view* grad_ys,
                        float* grad_hagg, void* grad_bias,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Per-token polynomial features (pom/pom.py:83-88), the operand of the
+ * dense (B, M, N) mask route (full_mask_mixer, pom/pom.py:41-45, whose mixing
+ * is a batched GEMM left to the GEMM library):
+ *   out[b, n, c] = sum_{j<K} coeff[c, j] act(x[b, n, c])^(j+1)
+ * coeff: (P, K) in param_dtype; x, out, grad views (B, N, P).
+ * ------------------------------------------------------------------------ */
+size_t pom_features_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int K);
+
+int pom_features_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                     const pom_view* x, const void* coeff, const pom_view* out, void* stream);
+
+/* Backward: grad_x = grad_out * p'(h) * act'(x); grad_coeff (P, K) in
+ * param_dtype = sum over tokens of grad_out * h^(j+1). */
+int pom_features_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                     const pom_view* x, const void* coeff, const pom_view* grad_out,
+                     const pom_view* grad_x, void* grad_coeff,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Operand layout

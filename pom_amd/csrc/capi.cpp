@@ -417,6 +417,59 @@ int setup_heads(pom::HeadsParams& p, int dtype, int param_dtype, int64_t B, int6
   return POM_OK;
 }
 
+// Polynomial-feature geometry: chunk width V (<= 16 bytes, aligned, and at
+// most 32 / KM so the per-thread coefficient and gradient arrays stay in
+// registers) and token chunks.
+int features_km(int K) { return K <= 4 ? K : (K <= 8 ? 8 : 16); }
+
+void features_chunks(int64_t B, int64_t N, int64_t P, int V, int64_t& RC, int64_t& nch) {
+  const int64_t cols = cdiv(P / V, 256);
+  int64_t cpf = 1;
+  while (B * cols * cpf < tune().target_wg && cdiv(N, 2 * cpf) >= 16) cpf *= 2;
+  RC = cdiv(N, cpf);
+  nch = cdiv(N, RC);
+}
+
+size_t features_ws_bytes(int64_t B, int64_t N, int64_t P, int K) {
+  int64_t nch = 1;
+  for (int V : {1, 2, 4, 8}) {
+    int64_t rc, n;
+    features_chunks(B, N, P, V, rc, n);
+    if (n > nch) nch = n;
+  }
+  return carve_bytes({B * nch * (int64_t)K * P});
+}
+
+int setup_features(pom::FeatParams& p, int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                   const pom_view* x, const void* coeff, std::initializer_list<const pom_view*> views) {
+  if (int r = check_dtype(dtype)) return r;
+  if (check_dtype(param_dtype)) return fail(POM_ERR_INVALID, "bad param_dtype %d", param_dtype);
+  if (B <= 0 || N <= 0 || P <= 0) return fail(POM_ERR_INVALID, "empty shape");
+  if (K < 1 || K > POM_MAX_DEGREE) return fail(POM_ERR_UNSUPPORTED, "degree %d outside [1, %d]", K, POM_MAX_DEGREE);
+  if (int r = check_view(x, "x")) return r;
+  for (const pom_view* v : views)
+    if (int r = check_view(v, "features view")) return r;
+  if (!coeff) return fail(POM_ERR_INVALID, "coeff is null");
+  p.dtype = dtype; p.K = K; p.B = B; p.N = N; p.P = P;
+  p.x = x->data; p.sxb = x->stride_b; p.sxn = x->stride_n;
+  p.coeff = {coeff, param_dtype};
+  const int eb = elem_bytes(dtype);
+  int V = 16 / eb;
+  const int vmax = 32 / features_km(K) > 0 ? 32 / features_km(K) : 1;
+  while (V > vmax) V /= 2;
+  while (V > 1) {
+    bool ok = P % V == 0 && aligned(x->data, (int64_t)V * eb) && x->stride_b % V == 0 && x->stride_n % V == 0;
+    for (const pom_view* v : views)
+      ok = ok && aligned(v->data, (int64_t)V * eb) && v->stride_b % V == 0 && v->stride_n % V == 0;
+    if (ok) break;
+    V /= 2;
+  }
+  p.V = V;
+  features_chunks(B, N, P, V, p.RC, p.nch);
+  if (p.nch > 65535 || B > 65535) return fail(POM_ERR_UNSUPPORTED, "grid too large");
+  return POM_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -608,6 +661,42 @@ int pom_gate_heads_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::heads_bwd_t<decltype(t)>(p, st); }),
                     "pom_gate_heads_bwd launch");
+}
+
+size_t pom_features_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int K) {
+  if (check_dtype(dtype) || B <= 0 || N <= 0 || P <= 0 || K < 1 || K > POM_MAX_DEGREE) return 0;
+  return features_ws_bytes(B, N, P, K);
+}
+
+int pom_features_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                     const pom_view* x, const void* coeff, const pom_view* out, void* stream) {
+  pom::FeatParams p;
+  if (int r = check_view(out, "out")) return r;
+  if (int r = setup_features(p, dtype, param_dtype, B, N, P, K, x, coeff, {out})) return r;
+  p.out = out->data; p.sob = out->stride_b; p.son = out->stride_n;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return hip_status(by_dtype(dtype, [&](auto t) { return pom::features_fwd_t<decltype(t)>(p, st); }),
+                    "pom_features_fwd launch");
+}
+
+int pom_features_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                     const pom_view* x, const void* coeff, const pom_view* grad_out,
+                     const pom_view* grad_x, void* grad_coeff,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  pom::FeatParams p;
+  if (int r = check_view(grad_out, "grad_out")) return r;
+  if (int r = check_view(grad_x, "grad_x")) return r;
+  if (int r = setup_features(p, dtype, param_dtype, B, N, P, K, x, coeff, {grad_out, grad_x})) return r;
+  if (!grad_coeff) return fail(POM_ERR_INVALID, "grad_coeff is null");
+  p.go = grad_out->data; p.sgob = grad_out->stride_b; p.sgon = grad_out->stride_n;
+  p.gx = grad_x->data; p.sgxb = grad_x->stride_b; p.sgxn = grad_x->stride_n;
+  p.gc = {grad_coeff, param_dtype};
+  if (int r = need_ws(workspace, workspace_bytes, features_ws_bytes(B, N, P, K))) return r;
+  Carve c{static_cast<char*>(workspace), 0};
+  p.part = c.take<float>(B * p.nch * (int64_t)K * P);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return hip_status(by_dtype(dtype, [&](auto t) { return pom::features_bwd_t<decltype(t)>(p, st); }),
+                    "pom_features_bwd launch");
 }
 
 int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src, void* dst,

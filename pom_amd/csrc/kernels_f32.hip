@@ -3,6 +3,7 @@
 #include "scan_impl.h"
 #include "gate_impl.h"
 #include "heads_impl.h"
+#include "features_impl.h"
 
 namespace pom {
 template hipError_t agg_fwd_t<float>(const AggParams&, hipStream_t);
@@ -13,4 +14,6 @@ template hipError_t gate_fwd_t<float>(const GateParams&, int, hipStream_t);
 template hipError_t gate_bwd_t<float>(const GateParams&, int, hipStream_t);
 template hipError_t heads_fwd_t<float>(const HeadsParams&, hipStream_t);
 template hipError_t heads_bwd_t<float>(const HeadsParams&, hipStream_t);
+template hipError_t features_fwd_t<float>(const FeatParams&, hipStream_t);
+template hipError_t features_bwd_t<float>(const FeatParams&, hipStream_t);
 }  // namespace pom

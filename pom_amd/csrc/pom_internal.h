@@ -182,6 +182,31 @@ struct GateParams {
 template <typename T> hipError_t gate_fwd_t(const GateParams& p, int per_token, hipStream_t st);
 template <typename T> hipError_t gate_bwd_t(const GateParams& p, int per_token, hipStream_t st);
 
+// Per-token polynomial features p = poly(act(x)) and their backward (the
+// dense-mask route's operand).  One thread per V-channel chunk and chunk of
+// RC token rows.
+struct FeatParams {
+  int dtype = DT_BF16;
+  int K = 2;
+  int V = 1;
+  int64_t B = 0, N = 0, P = 0;
+  int64_t RC = 1, nch = 1;
+  const void* x = nullptr;        // (B, N, P) view
+  int64_t sxb = 0, sxn = 0;
+  ParamIn coeff;                  // (P, K)
+  void* out = nullptr;            // (B, N, P) view (forward)
+  int64_t sob = 0, son = 0;
+  const void* go = nullptr;       // (B, N, P) upstream gradient view (backward)
+  int64_t sgob = 0, sgon = 0;
+  void* gx = nullptr;             // (B, N, P) view
+  int64_t sgxb = 0, sgxn = 0;
+  ParamOut gc;                    // (P, K)
+  float* part = nullptr;          // (B, nch, K, P)
+};
+
+template <typename T> hipError_t features_fwd_t(const FeatParams& p, hipStream_t st);
+template <typename T> hipError_t features_bwd_t(const FeatParams& p, hipStream_t st);
+
 // Per-head gating (n_sel_heads = H > 1): sh[b,n,c] = rot(hardsigmoid(y_s + bias))[h] * hagg[b, n / L, c],
 // h = c / hd, P = H * hd.
 struct HeadsParams {

@@ -2,8 +2,9 @@
 reductions, run as GPU library operations (no CPU path).
 
 * Dense (B, M, N) masks — ``full_mask_mixer`` (pom/pom.py:41-45): the
-  per-token polynomial features are formed on the GPU and mixed with the mask
-  as one batched GEMM on the matrix cores, divided by the mask's row sums.
+  per-token polynomial features come from the HIP feature kernels and are
+  mixed with the mask as one batched GEMM on the matrix cores, divided by the
+  mask's row sums.
   This is O(M * N * P) by nature; frame-causal video masks should use the
   O(N) ``block_causal(frame_len)`` descriptor instead.
 
@@ -13,20 +14,14 @@ gives the reference's gradients.
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
-from . import _lib
+from . import ops
 
 
 def poly_features(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
-    """(B, N, P) -> (B, N, P) per-token p(act(x)) — pom/pom.py:83-88."""
-    _lib.require_device(x)
-    h = torch.clamp(F.leaky_relu(x, 0.01), min=-0.1, max=6).unsqueeze(-1)
-    hp, powers = h, [h]
-    for _ in range(k - 1):
-        hp = hp * h
-        powers.append(hp)
-    return (torch.cat(powers, dim=-1) * coeff.to(x.dtype)).sum(-1)
+    """(B, N, P) -> (B, N, P) per-token p(act(x)) — pom/pom.py:83-88 — on the
+    HIP feature kernels (pom_features_fwd / _bwd)."""
+    return ops.poly_features_hip(x, coeff, k)
 
 
 def full_mask_mix(h: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:

@@ -295,6 +295,41 @@ def gate_backward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Te
     return gh, gb
 
 
+def features_forward(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
+    """Per-token polynomial features poly(act(x)) (B, N, P) in x.dtype, via
+    pom_features_fwd."""
+    lib = _lib.load()
+    B, N, P = x.shape
+    out = torch.empty(B, N, P, dtype=x.dtype, device=x.device)
+    xv, ov = view3(x), view3(out)
+    with _Span("features_fwd"):
+        rc = lib.pom_features_fwd(dtype_code(x), _pdt(coeff), B, N, P, k, ctypes.byref(xv), coeff.data_ptr(),
+                                  ctypes.byref(ov), stream_handle(x.device))
+    check(rc, "pom_features_fwd")
+    return out
+
+
+def features_backward(x: torch.Tensor, coeff: torch.Tensor, k: int, grad_out: torch.Tensor):
+    """Returns (grad_x in x.dtype, grad_coeff in coeff.dtype) via pom_features_bwd."""
+    lib = _lib.load()
+    B, N, P = x.shape
+    if grad_out.dtype != x.dtype:
+        grad_out = grad_out.to(x.dtype)
+    if grad_out.stride(2) != 1:
+        grad_out = grad_out.contiguous()
+    gx = torch.empty(B, N, P, dtype=x.dtype, device=x.device)
+    gc = torch.empty(P, k, dtype=coeff.dtype, device=x.device)
+    dt = dtype_code(x)
+    ws = workspace(x.device, lib.pom_features_workspace_size(dt, B, N, P, k))
+    xv, gv, dv = view3(x), view3(grad_out), view3(gx)
+    with _Span("features_bwd"):
+        rc = lib.pom_features_bwd(dt, _pdt(coeff), B, N, P, k, ctypes.byref(xv), coeff.data_ptr(),
+                                  ctypes.byref(gv), ctypes.byref(dv), gc.data_ptr(), ws.data_ptr(), ws.numel(),
+                                  stream_handle(x.device))
+    check(rc, "pom_features_bwd")
+    return gx, gc
+
+
 def gate_heads_forward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor, heads: int,
                        rope: Optional[RopeSpec] = None) -> torch.Tensor:
     """Per-head gating (n_sel_heads = heads > 1) via pom_gate_heads_fwd:
@@ -382,6 +417,29 @@ def _mask32(mask: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     if mask.shape != (B, N):
         raise ValueError(f"mask must have shape ({B}, {N}), got {tuple(mask.shape)}")
     return mask.to(device=x.device, dtype=torch.float32).contiguous()
+
+
+class _Features(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, coeff, k):
+        _lib.require_device(x)
+        c = _coeff_param(coeff, x.shape[2], k)
+        ctx.save_for_backward(x, c)
+        ctx.k, ctx.coeff_dtype = k, coeff.dtype
+        return features_forward(x, c, k)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, c = ctx.saved_tensors
+        gx, gc = features_backward(x, c, ctx.k, grad_out)
+        return gx, gc.to(ctx.coeff_dtype), None
+
+
+def poly_features_hip(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
+    """(B, N, P) -> (B, N, P) per-token p(act(x)) — pom/pom.py:83-88 — on the
+    HIP kernels (the dense-mask route's operand)."""
+    _check_degree(k)
+    return _Features.apply(x, coeff, k)
 
 
 def poly_agg_mean_hip(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:

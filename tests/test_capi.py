@@ -33,7 +33,8 @@ def test_header_lists_expected_entry_points():
     names = _declared_functions()
     for n in ["pom_abi_version", "pom_last_error", "pom_agg_workspace_size", "pom_agg_fwd", "pom_agg_bwd",
               "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd", "pom_gate_heads_workspace_size",
-              "pom_gate_heads_fwd", "pom_gate_heads_bwd", "pom_transpose"]:
+              "pom_gate_heads_fwd", "pom_gate_heads_bwd", "pom_features_workspace_size", "pom_features_fwd",
+              "pom_features_bwd", "pom_transpose"]:
         assert n in names
 
 
@@ -238,4 +239,21 @@ def test_heads_validation_before_launch(lib):
     assert need > 0 and lib.pom_gate_heads_workspace_size(1, 2, 64, 64, 7, 1) == 0
     rc = lib.pom_gate_heads_bwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 1, None, sh, ys, ctypes.c_void_p(1 << 16),
                                 None, ctypes.c_void_p(1 << 20), need - 1, None)
+    assert rc == _lib.POM_ERR_WORKSPACE
+
+
+def test_features_validation_before_launch(lib):
+    from pom_amd import _lib
+    x = ctypes.byref(_view(256, 64 * 32, 32))
+    out = ctypes.byref(_view(8192, 64 * 32, 32))
+    rc = lib.pom_features_fwd(1, 1, 2, 64, 32, 17, x, ctypes.c_void_p(512), out, None)
+    assert rc == _lib.POM_ERR_UNSUPPORTED and b"degree" in lib.pom_last_error()
+    rc = lib.pom_features_fwd(1, 1, 2, 64, 32, 2, x, None, out, None)
+    assert rc == _lib.POM_ERR_INVALID and b"coeff" in lib.pom_last_error()
+    rc = lib.pom_features_fwd(5, 1, 2, 64, 32, 2, x, ctypes.c_void_p(512), out, None)
+    assert rc == _lib.POM_ERR_INVALID
+    need = lib.pom_features_workspace_size(1, 2, 64, 32, 2)
+    assert need > 0 and lib.pom_features_workspace_size(1, 2, 64, 32, 0) == 0
+    rc = lib.pom_features_bwd(1, 1, 2, 64, 32, 2, x, ctypes.c_void_p(512), out, out, ctypes.c_void_p(1024),
+                              ctypes.c_void_p(1 << 20), need - 1, None)
     assert rc == _lib.POM_ERR_WORKSPACE
