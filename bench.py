@@ -46,6 +46,9 @@ CONFIGS = {
                         "degree=2, expand=4)"),
     "c5": dict(B=8, N=4096, D=1536, K=2, E=2, variant="rope2d", H=64, W=64,
                workload="C5 2-D RoPE PoM layer fwd+bwd (B=8, N=4096 on 64x64, D=1536, degree=2, expand=2)"),
+    # the reference's own benchmarks gate per head (n_sel_heads = num_heads = 16)
+    "c2h": dict(B=16, N=1024, D=1152, K=2, E=2, variant="mean", heads=16,
+                workload="C2 PoM layer fwd+bwd with n_sel_heads=16 (B=16, N=1024, D=1152, degree=2, expand=2)"),
 }
 
 
@@ -102,10 +105,11 @@ def make_module(cfg):
     import torch
     import pom_amd
     torch.manual_seed(0)
+    heads = cfg.get("heads", 1)
     if cfg["variant"] == "rope2d":
-        return pom_amd.PoMRoPE(cfg["D"], cfg["K"], cfg["E"], 1, 1, False, max_h=cfg["H"], max_w=cfg["W"],
+        return pom_amd.PoMRoPE(cfg["D"], cfg["K"], cfg["E"], 1, heads, False, max_h=cfg["H"], max_w=cfg["W"],
                                rope_2d=True)
-    return pom_amd.PoM(cfg["D"], cfg["K"], cfg["E"], 1, 1, False)
+    return pom_amd.PoM(cfg["D"], cfg["K"], cfg["E"], 1, heads, False)
 
 
 def forward_fn(cfg, extra_dev):
@@ -159,6 +163,10 @@ def kernel_work(cfg, extra):
         "gate_fwd": ("hbm", float(2 * T * P * e + cm + B * G * P * 4)),
         # y_s and dsh read, dy_s (and its channel-major copy) written
         "gate_bwd": ("hbm", float(3 * T * P * e + cm + B * G * P * 4)),
+        # per-head gate: sh written (y_s and hagg are H / P wide per token / row)
+        "gate_heads_fwd": ("hbm", float(T * P * e + T * cfg.get("heads", 1) * e + B * G * P * e)),
+        # dsh read once, y_s read, dy_s written, fp32 dhagg written
+        "gate_heads_bwd": ("hbm", float(T * P * e + 2 * T * cfg.get("heads", 1) * e + B * G * P * 4)),
         # operand-layout transposes for the backward GEMMs: read + write once
         "transpose_x": ("hbm", float(2 * T * D * e)),
         "transpose_sh": ("hbm", float(2 * T * P * e)),
@@ -302,7 +310,7 @@ def cpu_run(cfg, budget_s: float):
     x, go, extra = make_inputs(cfg)
     torch.manual_seed(0)
     rope2d = True if cfg["variant"] == "rope2d" else None
-    prm = O.init_params(cfg["D"], cfg["K"], cfg["E"], rope_2d=rope2d,
+    prm = O.init_params(cfg["D"], cfg["K"], cfg["E"], n_sel_heads=cfg.get("heads", 1), rope_2d=rope2d,
                         max_h=cfg.get("H", 64), max_w=cfg.get("W", 64))
     for t in (prm.w_qc, prm.se_bias, prm.po_coeff, prm.w_ag):
         t.requires_grad_(True)
@@ -354,6 +362,8 @@ KERNEL_NAMES = {
     "gate_fwd": ["gate_fwd_kernel"],
     "gate_bwd": ["gate_bwd_kernel", "gate_bwd_finalize"],
     "transpose": ["transpose_blocks", "transpose_elems"],   # x^T, g^T and the weights, per step
+    "gate_heads_fwd": ["heads_fwd_kernel"],
+    "gate_heads_bwd": ["heads_bwd_token_kernel", "heads_bwd_hagg_kernel", "heads_bwd_finalize"],
 }
 
 
@@ -543,7 +553,8 @@ def main():
         "roofline": roofline, "kernels": kernels,
     }
     if kernels:
-        agg = [n for n in ("agg_fwd", "agg_bwd", "gate_fwd", "gate_bwd") if n in kernels]
+        agg = [n for n in ("agg_fwd", "agg_bwd", "gate_fwd", "gate_bwd", "gate_heads_fwd", "gate_heads_bwd")
+               if n in kernels]
         gem = [n for n in kernels if n.startswith("gemm")]
         t_hbm = sum(kernels[n]["us_per_step"] for n in agg)
         t_mf = sum(kernels[n]["us_per_step"] for n in gem)

@@ -352,8 +352,9 @@ def gate_heads_forward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: tor
 
 def gate_heads_backward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor,
                         grad_sh: torch.Tensor, heads: int, rope: Optional[RopeSpec] = None,
-                        want_bias: bool = True):
-    """Returns (grad_ys (B, N, heads) in ys.dtype, grad_hagg (B, G, P) fp32,
+                        want_bias: bool = True, grad_ys: Optional[torch.Tensor] = None):
+    """Returns (grad_ys (B, N, heads) in ys.dtype — written into ``grad_ys``
+    when given, e.g. the gate slice of dY — grad_hagg (B, G, P) fp32,
     grad_bias (heads,) in bias.dtype or None) via pom_gate_heads_bwd."""
     lib = _lib.load()
     B, N, H = ys.shape
@@ -364,7 +365,7 @@ def gate_heads_backward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: to
     if grad_sh.stride(2) != 1:
         grad_sh = grad_sh.contiguous()
     dt = dtype_code(ys)
-    gys = torch.empty(B, N, H, dtype=ys.dtype, device=ys.device)
+    gys = torch.empty(B, N, H, dtype=ys.dtype, device=ys.device) if grad_ys is None else grad_ys
     gh = torch.empty(B, G, P, dtype=torch.float32, device=ys.device)
     gb = torch.empty(H, dtype=bias.dtype if bias is not None else torch.float32,
                      device=ys.device) if want_bias else None
@@ -566,14 +567,13 @@ def gate_heads_hip(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.T
 # ---------------------------------------------------------------------------
 
 class _PoMLayer(torch.autograd.Function):
-    """Self-mixing PoM layer (n_groups == 1, n_sel_heads <= 1) — pom/pom.py:216-231
-    composed with _get_h_s (:204-207), pom() (:125-135) and, for RoPE,
-    pom/pom_rope.py:476-526.
+    """Self-mixing PoM layer (n_groups == 1) — pom/pom.py:216-231 composed with
+    _get_h_s (:204-207), pom() (:125-135) and, for RoPE, pom/pom_rope.py:476-526.
 
-    Memory plan (T = B*N tokens):
-      forward : Y = x W_qc^T (T, 2P) -> hagg (B, G, P) -> sh (T, P) -> out (T, D)
-      backward: dsh = g W_ag (T, P); dY (T, 2P) is filled in two halves by the
-                gate (s-half) and aggregation (h-half) kernels, then
+    Memory plan (T = B*N tokens, S = P gate channels, or H = n_sel_heads):
+      forward : Y = x W_qc^T (T, P+S) -> hagg (B, G, P) -> sh (T, P) -> out (T, D)
+      backward: dsh = g W_ag (T, P); dY (T, P+S) is filled in two parts by the
+                gate (s-part) and aggregation (h-part) kernels, then
                 dx = dY W_qc and dW_qc = dY^T x.
     In 16-bit training (_NT_GEMMS) the weight gradients are dW_ag = g^T sh
     and dW_qc = dY^T x on token-contiguous copies (gt, sht, dyt, xt) and the
@@ -588,10 +588,11 @@ class _PoMLayer(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, mask, rope_h, rope_s, carry, n_past,
-                training):
+                training, heads):
         _lib.require_device(x)
         B, N, D = x.shape
         P = coeff.shape[0]
+        S = heads if heads > 1 else P
         T = B * N
         dt = x.dtype
         dev = x.device
@@ -608,16 +609,20 @@ class _PoMLayer(torch.autograd.Function):
                 xt = transpose(x2, "transpose_x")                  # (D, T), overlaps qc_fwd
         wq = w_qc if w_qc.dtype == dt else w_qc.to(dt)
         with _Span("gemm_qc_fwd"), tuned_gemms():
-            y = torch.mm(x2, wq.t())                                # (T, 2P)
-        y3 = y.view(B, N, 2 * P)
+            y = torch.mm(x2, wq.t())                                # (T, P+S)
+        y3 = y.view(B, N, P + S)
         h_view, s_view = y3[..., :P], y3[..., P:]
         c32 = _coeff_param(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
         b32 = _param(se_bias)
-        fused = want_sht and _NT_COPIES == "fused"
+        # the per-head gate writes no channel-major copy: sh^T comes from the transpose kernel
+        fused = want_sht and _NT_COPIES == "fused" and heads <= 1
         if fused:
             sht = torch.empty(P, T, dtype=dt, device=dev)
-        sh = gate_forward(s_view, b32, hagg, rope_s, out_t=sht if fused else None)   # (B, N, P)
+        if heads > 1:
+            sh = gate_heads_forward(s_view, b32, hagg, heads, rope_s)             # (B, N, P)
+        else:
+            sh = gate_forward(s_view, b32, hagg, rope_s, out_t=sht if fused else None)   # (B, N, P)
         if want_sht and not fused:
             side.wait_stream(cur)
             with torch.cuda.stream(side):
@@ -639,7 +644,7 @@ class _PoMLayer(torch.autograd.Function):
                               hagg, c32, b32, wq, wa, mask, count)
         ctx.shape = (B, N, D)
         ctx.set_materialize_grads(False)   # the aggregate output is usually unused
-        ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None)
+        ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None, heads)
         ctx.dtypes = (w_qc.dtype, se_bias.dtype, coeff.dtype, w_ag.dtype,
                       None if b_ag is None else b_ag.dtype)
         return out.view(B, N, D), hagg
@@ -647,13 +652,14 @@ class _PoMLayer(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out, grad_hagg):
         x, xt, y, sh, sht, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
-        k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias = ctx.meta
+        k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias, heads = ctx.meta
         B, N, D = ctx.shape
         dev = y.device
         dt = y.dtype
         if grad_out is None:   # only the aggregate was used downstream
             grad_out = torch.zeros(B, N, D, dtype=dt, device=dev)
         P = c32.shape[0]
+        S = heads if heads > 1 else P
         T = B * N
         need_x, need_wq, need_wa = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[4]
         nt_a = xt is not None or sht is not None   # token-contiguous weight gradients
@@ -690,14 +696,20 @@ class _PoMLayer(torch.autograd.Function):
                 with _Span("gemm_ag_wgrad"), tuned_gemms():
                     dw_ag = torch.mm(g2.t(), sh.view(T, P))         # (D, P)
         db_ag = g2.float().sum(0) if has_bias else None
-        y3 = y.view(B, N, 2 * P)
-        dy = torch.empty(T, 2 * P, dtype=dt, device=dev)
-        dy3 = dy.view(B, N, 2 * P)
+        y3 = y.view(B, N, P + S)
+        dy = torch.empty(T, P + S, dtype=dt, device=dev)
+        dy3 = dy.view(B, N, P + S)
         want_dyt = need_wq and xt is not None
         fused = want_dyt and _NT_COPIES == "fused"
-        dyt = torch.empty(2 * P, T, dtype=dt, device=dev) if fused else None
-        dh, dbias = gate_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), dy3[..., P:], rope_s,
-                                  grad_ys_t=None if dyt is None else dyt[P:], grad_ys_rows=dy[:, P:])
+        dyt = torch.empty(P + S, T, dtype=dt, device=dev) if fused else None
+        if heads > 1:
+            _, dh, dbias = gate_heads_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), heads, rope_s,
+                                               grad_ys=dy3[..., P:])
+            if dyt is not None:   # the gate part of dY^T (H rows) from the transpose kernel
+                _transpose_into(dy[:, P:], dyt[P:], "transpose_dy")
+        else:
+            dh, dbias = gate_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), dy3[..., P:], rope_s,
+                                      grad_ys_t=None if dyt is None else dyt[P:], grad_ys_rows=dy[:, P:])
         if grad_hagg is not None:
             dh = dh + grad_hagg.float()
         dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h,
@@ -705,15 +717,15 @@ class _PoMLayer(torch.autograd.Function):
         if want_dyt and not fused:
             side.wait_stream(cur)
             with torch.cuda.stream(side):
-                dyt = transpose(dy, "transpose_dy")                # (2P, T), overlaps qc_dgrad
+                dyt = transpose(dy, "transpose_dy")                # (P+S, T), overlaps qc_dgrad
         dw_qc = None
         if need_wq and want_dyt and over:
             side.wait_stream(cur)                                   # dY^T is complete
             with torch.cuda.stream(side), _Span("gemm_qc_wgrad"), tuned_gemms():
-                dw_qc = torch.mm(dyt, xt.t())                       # (2P, D), on the second stream
+                dw_qc = torch.mm(dyt, xt.t())                       # (P+S, D), on the second stream
         dx = None
         if need_x:
-            wq_k = _weight_t(wq).t() if nt else wq                  # (2P, D), K-contiguous when nt
+            wq_k = _weight_t(wq).t() if nt else wq                  # (P+S, D), K-contiguous when nt
             with _Span("gemm_qc_dgrad"), tuned_gemms():
                 dx = torch.mm(dy, wq_k)                             # (T, D)
         if need_wq and dw_qc is None:
@@ -722,10 +734,10 @@ class _PoMLayer(torch.autograd.Function):
                     cur.wait_stream(side)
                     dyt.record_stream(cur)
                 with _Span("gemm_qc_wgrad"), tuned_gemms():
-                    dw_qc = torch.mm(dyt, xt.t())                   # (2P, D)
+                    dw_qc = torch.mm(dyt, xt.t())                   # (P+S, D)
             else:
                 with _Span("gemm_qc_wgrad"), tuned_gemms():
-                    dw_qc = torch.mm(dy.t(), x.reshape(T, D))       # (2P, D)
+                    dw_qc = torch.mm(dy.t(), x.reshape(T, D))       # (P+S, D)
         if side is not None:
             cur.wait_stream(side)   # join before g2 or dy can be freed
             if over:
@@ -740,14 +752,15 @@ class _PoMLayer(torch.autograd.Function):
         tq, tb, tc, ta, tab = ctx.dtypes
         return (None if dx is None else dx.view(B, N, D), None if dw_qc is None else dw_qc.to(tq),
                 dbias.to(tb), dcoeff.to(tc), None if dw_ag is None else dw_ag.to(ta),
-                None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None, None)
+                None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None, None, None)
 
 
 def pom_layer(x, w_qc, se_bias, coeff, w_ag, b_ag, k: int, frame_len: Optional[int] = None,
               mask: Optional[torch.Tensor] = None, rope_h: Optional[RopeSpec] = None,
               rope_s: Optional[RopeSpec] = None, carry: Optional[torch.Tensor] = None,
-              n_past: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Run the fused layer; returns (out (B, N, D), hagg (B, G, P))."""
+              n_past: int = 0, heads: int = 1) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Run the fused layer; returns (out (B, N, D), hagg (B, G, P)).  heads > 1:
+    per-head gating (n_sel_heads), w_qc (P + heads, D), rope_s over the heads."""
     _check_degree(k)
     if not x.is_contiguous():
         x = x.contiguous()
@@ -757,4 +770,4 @@ def pom_layer(x, w_qc, se_bias, coeff, w_ag, b_ag, k: int, frame_len: Optional[i
         raise ValueError(f"frame_len {frame_len} must divide the sequence length {N}")
     m32 = None if mask is None else _mask32(mask, x)
     return _PoMLayer.apply(x, w_qc, se_bias, coeff, w_ag, b_ag, k, frame_len, m32, rope_h, rope_s,
-                           carry, n_past if carry is not None else 0, torch.is_grad_enabled())
+                           carry, n_past if carry is not None else 0, torch.is_grad_enabled(), heads)

@@ -131,7 +131,7 @@ class PoM(nn.Module):
 
     # ------------------------------------------------------------------
     def _fused_ok(self, xq, xc) -> bool:
-        return self.n_groups == 1 and self.n_sel_heads <= 1 and xq is xc
+        return self.n_groups == 1 and xq is xc
 
     def _h_and_gate_input(self, xq, xc):
         """Context projection h and gate pre-activation y_s (without se_bias) —
@@ -195,7 +195,8 @@ class PoM(nn.Module):
                                         (isinstance(mask, torch.Tensor) and mask.dim() == 2)):
             m = mask if isinstance(mask, torch.Tensor) else None
             out, _ = ops.pom_layer(xq, self.qc_proj.weight, self.se_bias, self.po_coeff,
-                                   self.ag_proj.weight, self.ag_proj.bias, self.order, fl, m)
+                                   self.ag_proj.weight, self.ag_proj.bias, self.order, fl, m,
+                                   heads=self.n_sel_heads)
             return out
         return self._mix(xq, xc, mask, fl)
 
@@ -219,7 +220,7 @@ class PoM(nn.Module):
         if self._fused_ok(xq, xc):
             out, h = ops.pom_layer(xq, self.qc_proj.weight, self.se_bias, self.po_coeff,
                                    self.ag_proj.weight, self.ag_proj.bias, self.order,
-                                   carry=carry, n_past=n_past)
+                                   carry=carry, n_past=n_past, heads=self.n_sel_heads)
             return out, {"h": h, "n": n_past + 1}
         h_raw, ys, bias = self._h_and_gate_input(xq, xc)
         h = ops.poly_agg_state_hip(h_raw, self.po_coeff, self.order, carry, n_past)

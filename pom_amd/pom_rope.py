@@ -167,14 +167,13 @@ class PoMRoPE(PoM):
         rope_h = self._spec(xc.shape[1], eff_ctx, eff_ctx_hw, xc.device)
         rot_h = lambda t: self._rope_torch(t, eff_ctx, eff_ctx_hw)
         fl = self._frame_len(mask, xc.shape[1])
-        if self._fused_ok(xq, xc) and (mask is None or fl is not None):
-            rope_s = self._spec(xq.shape[1], positions, positions_hw, xq.device)
+        spec_s = self._spec_heads if self.n_sel_heads > 1 else self._spec
+        rope_s = spec_s(xq.shape[1], positions, positions_hw, xq.device)
+        if self._fused_ok(xq, xc) and (mask is None or fl is not None or
+                                        (isinstance(mask, torch.Tensor) and mask.dim() == 2)):
+            m = mask if isinstance(mask, torch.Tensor) else None
             out, _ = ops.pom_layer(xq, self.qc_proj.weight, self.se_bias, self.po_coeff,
-                                   self.ag_proj.weight, self.ag_proj.bias, self.order, fl, None,
-                                   rope_h, rope_s)
+                                   self.ag_proj.weight, self.ag_proj.bias, self.order, fl, m,
+                                   rope_h, rope_s, heads=self.n_sel_heads)
             return out
-        if self.n_sel_heads > 1:
-            rope_s = self._spec_heads(xq.shape[1], positions, positions_hw, xq.device)
-        else:
-            rope_s = self._spec(xq.shape[1], positions, positions_hw, xq.device)
         return self._mix(xq, xc, mask, fl, rope_h, rope_s, rot_h)

@@ -104,16 +104,17 @@ def test_heads_c2_width(device):
 
 
 def test_heads_modules_use_the_kernels(device):
-    """PoM / PoMRoPE with n_sel_heads > 1 gate through pom_gate_heads_*."""
+    """PoM / PoMRoPE with n_sel_heads > 1 gate through pom_gate_heads_* (the
+    fused layer and the unfused route both call gate_heads_forward)."""
     torch.manual_seed(0)
     seen = []
-    orig = ops.gate_heads_hip
+    orig = ops.gate_heads_forward
 
     def spy(*a, **k):
         seen.append(a[3])
         return orig(*a, **k)
 
-    ops.gate_heads_hip = spy
+    ops.gate_heads_forward = spy
     try:
         m = pom_amd.PoM(32, 2, 2, 1, 8).to(device)
         m(torch.randn(2, 16, 32, device=device)).sum().backward()
@@ -121,5 +122,5 @@ def test_heads_modules_use_the_kernels(device):
         hw = torch.stack(torch.meshgrid(torch.arange(4), torch.arange(4), indexing="ij"), -1).reshape(-1, 2)
         r(torch.randn(2, 16, 32, device=device), positions_hw=hw.to(device)).sum().backward()
     finally:
-        ops.gate_heads_hip = orig
+        ops.gate_heads_forward = orig
     assert seen == [8, 8]

@@ -44,9 +44,9 @@ def _check_module(device, module, x, go, dtype, oracle_fn, module_fn, tol=None, 
     return errs
 
 
-def _pom(dim, degree, expand, dtype, seed=0, coeff_std=None, bias=False):
+def _pom(dim, degree, expand, dtype, seed=0, coeff_std=None, bias=False, heads=1):
     torch.manual_seed(seed)
-    m = pom_amd.PoM(dim, degree, expand, 1, 1, bias)
+    m = pom_amd.PoM(dim, degree, expand, 1, heads, bias)
     if coeff_std is not None:
         with torch.no_grad():
             m.po_coeff.copy_(torch.randn(m.po_coeff.shape, generator=torch.Generator().manual_seed(11)) * coeff_std)
@@ -172,9 +172,9 @@ def test_cross_mixing(device, dtype):
                   lambda m, xd: m(xd, xcd))
 
 
-def _rope_module(dim, degree, expand, dtype, rope_2d, seed=0, **kw):
+def _rope_module(dim, degree, expand, dtype, rope_2d, seed=0, heads=1, **kw):
     torch.manual_seed(seed)
-    m = pom_amd.PoMRoPE(dim, degree, expand, 1, 1, False, rope_2d=rope_2d, **kw)
+    m = pom_amd.PoMRoPE(dim, degree, expand, 1, heads, False, rope_2d=rope_2d, **kw)
     with torch.no_grad():
         m.po_coeff.copy_(torch.randn(m.po_coeff.shape, generator=torch.Generator().manual_seed(11)) * 0.1)
     return m.to(dtype)
@@ -213,3 +213,43 @@ def test_layer_deterministic(device):
         res.append([out.detach().clone(), xd.grad.clone()] + [p.grad.clone() for p in m.parameters()])
     for a, b in zip(*res):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mask", [None, "causal", "padding", "frames"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_heads_module(device, dtype, mask):
+    """n_sel_heads = 8 through the fused layer (per-head gate kernels; in 16-bit
+    training the gate part of dY^T comes from the transpose kernel)."""
+    B, N, D = 2, 128, 64
+    x, go = _inputs(B, N, D, dtype)
+    m = _pom(D, 2, 2, dtype, coeff_std=0.1, bias=True, heads=8)
+    if mask == "padding":
+        mk = torch.arange(N).view(1, N) < torch.tensor([128, 37]).view(B, 1)
+        omask, dmask = mk, mk.to(device)
+    elif mask == "frames":
+        omask, dmask = ("block_causal", 32), pom_amd.block_causal(32)
+    else:
+        omask = dmask = mask
+    _check_module(device, m, x, go, dtype, lambda p, xr: O.pom_forward(p, xr, mask=omask),
+                  lambda m, xd: m(xd, mask=dmask))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rope_2d", [False, True])
+def test_heads_rope_module(device, dtype, rope_2d):
+    """PoMRoPE with n_sel_heads = 8 and a padding mask: masked RoPE aggregation
+    and the per-head rotated gate, fused."""
+    H = W = 8
+    B, N, D = 2, H * W, 64
+    x, go = _inputs(B, N, D, dtype)
+    mk = torch.arange(N).view(1, N) < torch.tensor([N, 23]).view(B, 1)
+    if rope_2d:
+        pos = torch.stack(torch.meshgrid(torch.arange(H), torch.arange(W), indexing="ij"), -1).reshape(-1, 2)
+        m = _rope_module(D, 2, 2, dtype, True, heads=8, max_h=H, max_w=W)
+        _check_module(device, m, x, go, dtype, lambda p, xr: O.rope_forward(p, xr, mask=mk, positions_hw=pos),
+                      lambda m, xd: m(xd, mask=mk.to(device), positions_hw=pos.to(device)))
+    else:
+        pos = torch.randperm(2 * N, generator=torch.Generator().manual_seed(4))[:N]
+        m = _rope_module(D, 2, 2, dtype, False, heads=8, max_seq_len=2 * N)
+        _check_module(device, m, x, go, dtype, lambda p, xr: O.rope_forward(p, xr, mask=mk, positions=pos),
+                      lambda m, xd: m(xd, mask=mk.to(device), positions=pos.to(device)))
