@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 6
+#define POM_AMD_ABI_VERSION 7
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -184,9 +184,11 @@ int pom_gate_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P,
 size_t pom_gate_heads_workspace_size(int dtype, int64_t B, int64_t N, int64_t P, int64_t H,
                                      int64_t groups);
 
+/* sh_t: channel-major copy of sh, or NULL (16-bit types; built for P % 8 == 0
+ * and N % 8 == 0 with 16-byte-aligned operands, else POM_ERR_UNSUPPORTED). */
 int pom_gate_heads_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
                        const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
-                       const pom_rope* rope, const pom_view* sh, void* stream);
+                       const pom_rope* rope, const pom_view* sh, const pom_tview* sh_t, void* stream);
 
 /* Backward.  grad_ys: (B, N, H) view receiving dL/dy_s.  grad_hagg:
  * (B, groups, P) fp32.  grad_bias: (H,) in param_dtype or NULL. */

@@ -27,7 +27,7 @@ POM_ERR_DEVICE = 4
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
 MAX_DEGREE = 16
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # Every symbol include/pom_amd.h declares, with its ctypes signature.
 _c_i64 = ctypes.c_int64
@@ -68,7 +68,7 @@ SIGNATURES = {
                               _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "pom_gate_heads_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "pom_gate_heads_fwd": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR,
-                                    _PV, _c_vp]),
+                                    _PV, _PT, _c_vp]),
     "pom_gate_heads_bwd": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _PV, _c_vp, _c_vp, _c_i64, _PR,
                                     _PV, _PV, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "pom_features_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_int]),

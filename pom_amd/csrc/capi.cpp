@@ -367,6 +367,14 @@ HeadsGeom heads_geom(int64_t B, int64_t N, int64_t P, int64_t groups, int V) {
   return g;
 }
 
+// Tile path geometry: 64-token x 64-channel workgroups.
+constexpr int64_t kHeadTile = 64;
+
+int64_t heads_nhm(int64_t P, int64_t H) {
+  const int64_t hd = P / H, n = (kHeadTile - 1) / (hd > 0 ? hd : 1) + 2;
+  return n < H ? n : H;
+}
+
 size_t heads_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups) {
   int64_t nch = 1, tok_wgs = 1;
   for (int V : {1, 2, 4, 8}) {   // every chunk width the call may choose
@@ -374,7 +382,10 @@ size_t heads_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups
     if (g.nch > nch) nch = g.nch;
     tok_wgs = g.tok_wgs;
   }
-  return carve_bytes({B * N * H, tok_wgs * H, B * nch * P});
+  const size_t general = carve_bytes({B * N * H, tok_wgs * H, B * nch * P});
+  const int64_t nct = cdiv(P, kHeadTile), ntt = cdiv(N, kHeadTile);
+  const size_t tile = carve_bytes({B * N * nct * heads_nhm(P, H), B * ntt * P, B * N * H});
+  return general > tile ? general : tile;
 }
 
 int setup_heads(pom::HeadsParams& p, int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
@@ -414,6 +425,15 @@ int setup_heads(pom::HeadsParams& p, int dtype, int param_dtype, int64_t B, int6
   const HeadsGeom g = heads_geom(B, N, P, groups, V);
   p.tok_wgs = g.tok_wgs; p.RC = g.RC; p.cpf = g.cpf; p.nch = g.nch; p.L = g.L; p.G = g.G;
   if (p.nch > 65535 || B > 65535) return fail(POM_ERR_UNSUPPORTED, "grid too large");
+  // tile path: 8-element vectors on every P-wide operand, tiles inside one group
+  bool tile = P % 8 == 0 && (p.L == 1 || p.L % kHeadTile == 0) && aligned(hagg, 16) &&
+              cdiv(N, kHeadTile) <= 65535 && H <= 256 &&   // dz tile: kHeadTile x H floats of LDS
+              P / H >= 8;                                   // a tile touches at most 9 heads
+  for (const pom_view* v : views)
+    tile = tile && aligned(v->data, 16) && v->stride_b % 8 == 0 && v->stride_n % 8 == 0;
+  p.tile = tile ? 1 : 0;
+  p.ntt = cdiv(N, kHeadTile);
+  p.nhm = heads_nhm(P, H);
   return POM_OK;
 }
 
@@ -628,10 +648,16 @@ size_t pom_gate_heads_workspace_size(int dtype, int64_t B, int64_t N, int64_t P,
 
 int pom_gate_heads_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
                        const pom_view* ys, const void* bias, const void* hagg, int64_t groups,
-                       const pom_rope* rope, const pom_view* sh, void* stream) {
+                       const pom_rope* rope, const pom_view* sh, const pom_tview* sh_t, void* stream) {
   pom::HeadsParams p;
   if (int r = check_view(sh, "sh")) return r;
   if (int r = setup_heads(p, dtype, param_dtype, B, N, P, H, ys, bias, hagg, groups, rope, {sh})) return r;
+  if (sh_t) {
+    // written by the tile kernel in 16-byte token runs
+    const bool ok = p.tile && N % 8 == 0 && aligned(sh_t->data, 16) && sh_t->stride_c % 8 == 0 &&
+                    sh_t->stride_b % 8 == 0;
+    if (int r = set_tview(p.sht, sh_t, dtype, ok ? 8 : 1, B, N, "sh_t")) return r;
+  }
   p.sh = sh->data; p.shb = sh->stride_b; p.shn = sh->stride_n;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::heads_fwd_t<decltype(t)>(p, st); }),
@@ -653,11 +679,18 @@ int pom_gate_heads_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t
   p.dys = grad_ys->data; p.dyb = grad_ys->stride_b; p.dyn = grad_ys->stride_n;
   p.dhagg = grad_hagg;
   p.dbias = {grad_bias, param_dtype};
+  if (p.tile && !aligned(grad_hagg, 16)) p.tile = 0;   // per-token rows are stored 8 floats at a time
   if (int r = need_ws(workspace, workspace_bytes, heads_ws_bytes(B, N, P, H, groups))) return r;
   Carve c{static_cast<char*>(workspace), 0};
-  p.sgate = c.take<float>(B * N * H);
-  p.part_b = c.take<float>(p.tok_wgs * H);
-  p.part_h = c.take<float>(B * p.nch * P);
+  if (p.tile) {
+    p.dpart = c.take<float>(B * N * cdiv(P, kHeadTile) * p.nhm);
+    p.part_h = c.take<float>(B * p.ntt * P);
+    p.dzbuf = c.take<float>(B * N * H);
+  } else {
+    p.sgate = c.take<float>(B * N * H);
+    p.part_b = c.take<float>(p.tok_wgs * H);
+    p.part_h = c.take<float>(B * p.nch * P);
+  }
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::heads_bwd_t<decltype(t)>(p, st); }),
                     "pom_gate_heads_bwd launch");

@@ -12,11 +12,12 @@
 //   ds'[b,n,h]  = sum_{c in head h} dsh[b,n,c] * hagg[b,g,c]
 //   ds = R^T ds',  dz = ds * hardsigmoid'(z)  -> dY_s, dbias[h] = sum_{b,n} dz
 //   dhagg[b,g,c] = sum_{n in g} s'[b,n,c / hd] * dsh[b,n,c]
-// heads_bwd_token: one wave per token row forms the head sums from per-chunk
-// dot products staged in LDS (fixed order), then dz, dY_s, s' (fp32 scratch)
-// and workgroup bias partials.  heads_bwd_hagg: channel-parallel sums of
-// s' * dsh over each group's tokens, in chunks; heads_bwd_finalize adds the
-// chunk and bias partials in a fixed order.
+// Tile path (the common shapes): heads_fwd_tile / heads_bwd_tile below.
+// General path: heads_bwd_token: one wave per token row forms the head sums
+// from per-chunk dot products staged in LDS (fixed order), then dz, dY_s, s'
+// (fp32 scratch) and workgroup bias partials.  heads_bwd_hagg:
+// channel-parallel sums of s' * dsh over each group's tokens, in chunks;
+// heads_bwd_finalize adds the chunk and bias partials in a fixed order.
 #pragma once
 
 #include "agg_impl.h"
@@ -225,6 +226,303 @@ static __global__ void __launch_bounds__(kThreads) heads_bwd_finalize(const Head
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tile kernels: a workgroup owns kTT tokens of one batch row x kCT channels.
+// Used when P % 8 == 0 (8-element chunks), the operands admit 8-element
+// vectors, and every tile lies in one hagg group (L % kTT == 0) or groups are
+// single tokens (L == 1).  The gate values of the tile's tokens and heads are
+// formed once per tile; the backward reads dsh once, forming both the
+// per-head dot products (over the tile's channels) and the aggregate-gradient
+// sums (over its tokens) from an LDS copy.
+// ---------------------------------------------------------------------------
+constexpr int kTT = 64, kCT = 64;
+constexpr int kGM = kCT / 8 + 1;   // heads a kCT-channel tile can touch (head_dim >= 8 on this path)
+
+// Per-tile prologue: local head of each channel and the gate values s'[t][hi].
+template <typename T, int MODE>
+__device__ __forceinline__ void tile_gates(const HeadsParams& p, int64_t b, int64_t n0, int64_t c0, int nt, int nc,
+                                           int64_t& h0, int& nh, int* hidx, float* gs) {
+  h0 = c0 / p.hd;
+  nh = (int)((c0 + nc - 1) / p.hd - h0) + 1;
+  const int tid = threadIdx.x;
+  if (tid < nc) hidx[tid] = (int)((c0 + tid) / p.hd - h0);
+  const T* yb = reinterpret_cast<const T*>(p.ys) + b * p.ysb;
+  for (int i = tid; i < nt * nh; i += kThreads) {
+    const int t = i / nh, hi = i - t * nh;
+    const int64_t n = n0 + t;
+    gs[t * kGM + hi] = head_gate<T, MODE>(p, yb + n * p.ysn, n, h0 + hi);
+  }
+}
+
+template <typename T, int MODE, bool TR>
+__global__ void __launch_bounds__(kThreads) heads_fwd_tile(const HeadsParams p) {
+  constexpr int PITCH = kTT + 8;   // [channel][token] rows of 16-byte multiples, staggered banks
+  __shared__ float gs[kTT * kGM];
+  __shared__ int hidx[kCT];
+  __shared__ __attribute__((aligned(16))) T tt[TR ? kCT * PITCH : 8];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.z, n0 = (int64_t)blockIdx.y * kTT, c0 = (int64_t)blockIdx.x * kCT;
+  const int nt = (int)(p.N - n0 < kTT ? p.N - n0 : kTT), nc = (int)(p.P - c0 < kCT ? p.P - c0 : kCT);
+  // this thread's two chunks (t, j) = (i >> 3, i & 7), i = tid and tid + 256:
+  // their hagg rows are loaded before the gate values are formed, so the two
+  // memory latencies overlap
+  const int cj = nc / 8;
+  const T* hb = reinterpret_cast<const T*>(p.hagg) + c0;
+  constexpr int R = kTT * 8 / kThreads;
+  Pack<T, 8> hp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
+    if (t < nt && j < cj) hp[r].load(hb + (b * p.G + (n0 + t) / p.L) * p.P + j * 8);
+  }
+  int64_t h0;
+  int nh;
+  tile_gates<T, MODE>(p, b, n0, c0, nt, nc, h0, nh, hidx, gs);
+  __syncthreads();
+  T* ob = reinterpret_cast<T*>(p.sh) + b * p.shb + c0;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
+    if (t >= nt || j >= cj) continue;
+    const int cc = j * 8;
+    float o[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) o[v] = gs[t * kGM + hidx[cc + v]] * hp[r].get(v);
+    VecIO<T, 8>::store(ob + (n0 + t) * p.shn + cc, o);
+    if constexpr (TR) {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) tt[(cc + v) * PITCH + t] = from_f32<T>(o[v]);
+    }
+  }
+  if constexpr (TR) {
+    __syncthreads();
+    using Raw = typename RawVec<16>::type;
+    T* base = reinterpret_cast<T*>(p.sht.data) + b * p.sht.sb + n0;
+    const int tj = nt / 8;   // N % 8 == 0 on this path
+    for (int i = tid; i < nc * 8; i += kThreads) {
+      const int cc = i >> 3, k = i & 7;
+      if (k >= tj) continue;
+      *reinterpret_cast<Raw*>(base + (c0 + cc) * p.sht.ld + k * 8) =
+          *reinterpret_cast<const Raw*>(tt + cc * PITCH + k * 8);
+    }
+  }
+}
+
+template <typename T, int MODE>
+__global__ void __launch_bounds__(kThreads) heads_bwd_tile(const HeadsParams p) {
+  constexpr int DP = kCT + 1;   // fp32 tile pitch: conflict-free columns
+  __shared__ float gs[kTT * kGM];
+  __shared__ float pr[kTT * DP];      // s' * dsh (groups of kTT or more tokens)
+  __shared__ float cd[kTT * 8 * 2];   // per chunk: the dot product's parts on its first / second head
+  __shared__ float red[4 * kCT];
+  __shared__ int hidx[kCT];
+  const int tid = threadIdx.x;
+  const int64_t b = blockIdx.z, n0 = (int64_t)blockIdx.y * kTT, c0 = (int64_t)blockIdx.x * kCT;
+  const int nt = (int)(p.N - n0 < kTT ? p.N - n0 : kTT), nc = (int)(p.P - c0 < kCT ? p.P - c0 : kCT);
+  const bool per_token = p.L == 1;
+  const int cj = nc / 8;
+  const T* gb = reinterpret_cast<const T*>(p.dsh) + b * p.dsb + c0;
+  const T* hb = reinterpret_cast<const T*>(p.hagg) + b * p.G * p.P + c0;
+  // this thread's two chunks (t, j) = (i >> 3, i & 7), i = tid and tid + 256:
+  // dsh and hagg are loaded before the gate values are formed, so the memory
+  // latencies overlap
+  constexpr int R = kTT * 8 / kThreads;
+  Pack<T, 8> gp[R], hp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
+    if (t < nt && j < cj) {
+      gp[r].load(gb + (n0 + t) * p.dsn + j * 8);
+      hp[r].load(hb + (per_token ? n0 + t : n0 / p.L) * p.P + j * 8);
+    }
+  }
+  int64_t h0;
+  int nh;
+  tile_gates<T, MODE>(p, b, n0, c0, nt, nc, h0, nh, hidx, gs);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
+    if (t >= nt || j >= cj) continue;
+    const int cc = j * 8, ha = hidx[cc];
+    float pa = 0.0f, pb = 0.0f, o[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int hv = hidx[cc + v];
+      const float g = gp[r].get(v), d = g * hp[r].get(v);
+      if (hv == ha) pa += d;
+      else pb += d;
+      o[v] = gs[t * kGM + hv] * g;
+    }
+    cd[i * 2] = pa;
+    cd[i * 2 + 1] = pb;
+    if (per_token) {
+      store_f32<8>(p.dhagg + (b * p.G + n0 + t) * p.P + c0 + cc, o);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) pr[t * DP + cc + v] = o[v];
+    }
+  }
+  __syncthreads();
+  // per-head dot products of the tile's channels: d s'[t][hi] partial
+  const int64_t nct = (p.P + kCT - 1) / kCT;
+  for (int i = tid; i < nt * nh; i += kThreads) {
+    const int t = i / nh, hi = i - t * nh;
+    float d = 0.0f;
+    for (int j = 0; j < cj; ++j) {
+      const int ha = hidx[j * 8], hz = hidx[j * 8 + 7];
+      d += (ha == hi ? cd[(t * 8 + j) * 2] : 0.0f) + (hz == hi && hz != ha ? cd[(t * 8 + j) * 2 + 1] : 0.0f);
+    }
+    p.dpart[((b * p.N + n0 + t) * nct + blockIdx.x) * p.nhm + hi] = d;
+  }
+  if (!per_token) {
+    // the tile's sum over its tokens: four token quarters, then a fixed sum
+    const int c = tid & (kCT - 1), q = tid >> 6;
+    float a = 0.0f;
+    if (c < nc) {
+      const int te = (q + 1) * (kTT / 4) < nt ? (q + 1) * (kTT / 4) : nt;
+      for (int t = q * (kTT / 4); t < te; ++t) a += pr[t * DP + c];
+    }
+    red[q * kCT + c] = a;
+    __syncthreads();
+    if (tid < nc)
+      p.part_h[(b * p.ntt + blockIdx.y) * p.P + c0 + tid] =
+          ((red[tid] + red[kCT + tid]) + red[2 * kCT + tid]) + red[3 * kCT + tid];
+  }
+}
+
+// Per (token, head): d s' from the channel-tile partials, R^T, hardsigmoid',
+// dY_s; dz summed per head over the workgroup's kTT tokens (bias partial).
+constexpr int kDzT = 16;   // tokens per workgroup of the dz kernel (= rows per bias partial)
+
+template <typename T, int MODE>
+__global__ void __launch_bounds__(kThreads) heads_bwd_dz(const HeadsParams p) {
+  extern __shared__ float dzl[];   // [kDzT][H]
+  const int64_t ntok = p.B * p.N, tok0 = (int64_t)blockIdx.x * kDzT;
+  const int nt = (int)(ntok - tok0 < kDzT ? ntok - tok0 : kDzT);
+  const int H = (int)p.H;
+  const int64_t nct = (p.P + kCT - 1) / kCT;
+  for (int i = threadIdx.x; i < nt * H; i += kThreads) {
+    const int t = i / H, h = i - t * H;
+    const int64_t tok = tok0 + t;
+    const int64_t b = tok / p.N, n = tok - b * p.N;
+    auto dsp = [&](int64_t hh) {
+      const int64_t ca = hh * p.hd, cb = ca + p.hd - 1;
+      float s = 0.0f;
+      for (int64_t ct = ca / kCT; ct <= cb / kCT; ++ct)
+        s += p.dpart[(tok * nct + ct) * p.nhm + (hh - (ct * kCT) / p.hd)];
+      return s;
+    };
+    float ds = dsp(h);
+    if constexpr (MODE != MODE_PLAIN) {
+      int blk, table;
+      int64_t col, partner;
+      head_pair<MODE>(p.H, h, blk, col, partner, table);
+      float cs, sn;
+      table_cs(p.rope, table, n, col, cs, sn);
+      const float dq = dsp(partner);
+      ds = blk ? ds * cs - dq * sn : ds * cs + dq * sn;
+    }
+    const T* yrow = reinterpret_cast<const T*>(p.ys) + b * p.ysb + n * p.ysn;
+    const float z = to_f32<T>(yrow[h]) + (p.bias.ptr ? param_get(p.bias, h) : 0.0f);
+    const float dz = ds * hsig_grad(z);
+    reinterpret_cast<T*>(p.dys)[b * p.dyb + n * p.dyn + h] = from_f32<T>(dz);
+    dzl[i] = dz;
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < H; h += kThreads) {
+    float s = 0.0f;
+    for (int t = 0; t < nt; ++t) s += dzl[t * H + h];
+    p.dzbuf[blockIdx.x * p.H + h] = s;
+  }
+}
+
+// dhagg[b, g, c] = sum of the group's token-tile partials (groups of L >= kTT
+// tokens); dbias[h] = sum over every token of dz (one workgroup per head,
+// strided sums then a fixed tree).
+static __global__ void __launch_bounds__(kThreads) heads_tile_finalize(const HeadsParams p) {
+  __shared__ float red[kThreads];
+  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (p.L > 1 && idx < p.B * p.G * p.P) {
+    const int64_t c = idx % p.P, bg = idx / p.P, b = bg / p.G, g = bg - b * p.G;
+    const int64_t per = p.L / kTT;
+    const float* src = p.part_h + (b * p.ntt + g * per) * p.P + c;
+    float s = 0.0f;
+    int64_t k = 0;
+    for (; k + 8 <= per; k += 8) {   // eight loads in flight, summed in order
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = src[(k + q) * p.P];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) s += v[q];
+    }
+    for (; k < per; ++k) s += src[k * p.P];
+    p.dhagg[idx] = s;
+  }
+  if (p.dbias.ptr && blockIdx.x < p.H) {
+    const int64_t h = blockIdx.x, rows = (p.B * p.N + kDzT - 1) / kDzT;   // dz-kernel partials
+    float s = 0.0f;
+    for (int64_t r = threadIdx.x; r < rows; r += kThreads) s += p.dzbuf[r * p.H + h];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int off = kThreads / 2; off > 0; off >>= 1) {
+      if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) param_set(p.dbias, h, red[0]);
+  }
+}
+
+template <typename T, int MODE>
+hipError_t heads_tile_fwd_m(const HeadsParams& p, hipStream_t st) {
+  const dim3 grid((unsigned)((p.P + kCT - 1) / kCT), (unsigned)((p.N + kTT - 1) / kTT), (unsigned)p.B);
+  if constexpr (sizeof(T) == 2) {
+    if (p.sht.data) {
+      hipLaunchKernelGGL((heads_fwd_tile<T, MODE, true>), grid, dim3(kThreads), 0, st, p);
+      return hipGetLastError();
+    }
+  } else {
+    if (p.sht.data) return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL((heads_fwd_tile<T, MODE, false>), grid, dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T, int MODE>
+hipError_t heads_tile_bwd_m(const HeadsParams& p, hipStream_t st) {
+  const dim3 grid((unsigned)((p.P + kCT - 1) / kCT), (unsigned)((p.N + kTT - 1) / kTT), (unsigned)p.B);
+  hipLaunchKernelGGL((heads_bwd_tile<T, MODE>), grid, dim3(kThreads), 0, st, p);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  const int64_t nb = (p.B * p.N + kDzT - 1) / kDzT;
+  hipLaunchKernelGGL((heads_bwd_dz<T, MODE>), dim3((unsigned)nb), dim3(kThreads),
+                     sizeof(float) * kDzT * (size_t)p.H, st, p);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  const int64_t flat = p.L > 1 ? (p.B * p.G * p.P + kThreads - 1) / kThreads : 0;
+  const int64_t fb = flat > p.H ? flat : (p.dbias.ptr ? p.H : flat);
+  if (fb > 0) hipLaunchKernelGGL(heads_tile_finalize, dim3((unsigned)fb), dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t heads_tile_fwd(const HeadsParams& p, hipStream_t st) {
+  switch (p.mode) {
+    case MODE_PLAIN: return heads_tile_fwd_m<T, MODE_PLAIN>(p, st);
+    case MODE_ROPE1D: return heads_tile_fwd_m<T, MODE_ROPE1D>(p, st);
+    case MODE_ROPE2D: return heads_tile_fwd_m<T, MODE_ROPE2D>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename T>
+hipError_t heads_tile_bwd(const HeadsParams& p, hipStream_t st) {
+  switch (p.mode) {
+    case MODE_PLAIN: return heads_tile_bwd_m<T, MODE_PLAIN>(p, st);
+    case MODE_ROPE1D: return heads_tile_bwd_m<T, MODE_ROPE1D>(p, st);
+    case MODE_ROPE2D: return heads_tile_bwd_m<T, MODE_ROPE2D>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 template <typename T, int V>
 hipError_t heads_fwd_v(const HeadsParams& p, hipStream_t st) {
   const int64_t total = p.B * p.N * (p.P / V);
@@ -273,11 +571,14 @@ hipError_t heads_bwd_v(const HeadsParams& p, hipStream_t st) {
 
 template <typename T>
 hipError_t heads_fwd_t(const HeadsParams& p, hipStream_t st) {
+  if (p.tile) return heads_tile_fwd<T>(p, st);
+  if (p.sht.data) return hipErrorInvalidValue;
   POM_V_SWITCH(T, p.V, heads_fwd_v, p, st)
 }
 
 template <typename T>
 hipError_t heads_bwd_t(const HeadsParams& p, hipStream_t st) {
+  if (p.tile) return heads_tile_bwd<T>(p, st);
   POM_V_SWITCH(T, p.V, heads_bwd_v, p, st)
 }
 

@@ -232,11 +232,21 @@ struct HeadsParams {
   float* dhagg = nullptr;         // (B, G, P) fp32
   ParamOut dbias;                 // (H,); ptr null: not wanted
 
+  TrOut sht;                      // channel-major copy of sh (tile path, 16-bit), or none
+
+  // general path
   int64_t tok_wgs = 1;            // workgroups of the token-row kernel (= bias partial rows)
   int64_t RC = 1, cpf = 1, nch = 1;   // aggregate-gradient chunks: cpf chunks of RC rows per group
   float* sgate = nullptr;         // (B, N, H) fp32 rotated gate values
   float* part_b = nullptr;        // (tok_wgs, H)
-  float* part_h = nullptr;        // (B, nch, P)
+  float* part_h = nullptr;        // (B, nch, P) | tile path: (B, ntt, P) token-tile partials
+
+  // tile path (64 tokens x 64 channels per workgroup)
+  int tile = 0;
+  int64_t ntt = 1;                // token tiles per batch row
+  int64_t nhm = 1;                // heads a channel tile can touch (dot-partial stride)
+  float* dpart = nullptr;         // (B * N, channel tiles, nhm) per-head dot partials
+  float* dzbuf = nullptr;         // (cdiv(B * N, 16), H) fp32 dz sums per 16-token group
 };
 
 // LDS of the token-row backward kernel: per wave, cpr chunk dots and two

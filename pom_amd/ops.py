@@ -331,10 +331,11 @@ def features_backward(x: torch.Tensor, coeff: torch.Tensor, k: int, grad_out: to
 
 
 def gate_heads_forward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.Tensor, heads: int,
-                       rope: Optional[RopeSpec] = None) -> torch.Tensor:
+                       rope: Optional[RopeSpec] = None, out_t: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Per-head gating (n_sel_heads = heads > 1) via pom_gate_heads_fwd:
     sh[b, n, c] = R hardsigmoid(ys + bias)[b, n, c // (P / heads)] * hagg[b, group(n), c].
-    ys (B, N, heads) view; hagg (B, G, P); rope over the heads gate channels."""
+    ys (B, N, heads) view; hagg (B, G, P); rope over the heads gate channels;
+    with out_t (P, B*N), also the channel-major copy of sh."""
     lib = _lib.load()
     B, N, H = ys.shape
     if H != heads:
@@ -343,10 +344,14 @@ def gate_heads_forward(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: tor
     G, P = hagg.shape[1], hagg.shape[2]
     sh = torch.empty(B, N, P, dtype=ys.dtype, device=ys.device)
     yv, sv = view3(ys), view3(sh)
-    with _Span("gate_heads_fwd"):
-        rc = lib.pom_gate_heads_fwd(dtype_code(ys), _pdt(bias), B, N, P, H, ctypes.byref(yv), ptr(bias),
-                                    hagg.data_ptr(), G, rope_ptr(rope), ctypes.byref(sv), stream_handle(ys.device))
-    check(rc, "pom_gate_heads_fwd")
+
+    def call(tv):
+        with _Span("gate_heads_fwd"):
+            return lib.pom_gate_heads_fwd(dtype_code(ys), _pdt(bias), B, N, P, H, ctypes.byref(yv), ptr(bias),
+                                          hagg.data_ptr(), G, rope_ptr(rope), ctypes.byref(sv), tv,
+                                          stream_handle(ys.device))
+    _with_copy(call, out_t, sh.view(B * N, P) if out_t is not None else None, "transpose_sh",
+               "pom_gate_heads_fwd", B, N)
     return sh
 
 
@@ -615,12 +620,11 @@ class _PoMLayer(torch.autograd.Function):
         c32 = _coeff_param(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
         b32 = _param(se_bias)
-        # the per-head gate writes no channel-major copy: sh^T comes from the transpose kernel
-        fused = want_sht and _NT_COPIES == "fused" and heads <= 1
+        fused = want_sht and _NT_COPIES == "fused"
         if fused:
             sht = torch.empty(P, T, dtype=dt, device=dev)
         if heads > 1:
-            sh = gate_heads_forward(s_view, b32, hagg, heads, rope_s)             # (B, N, P)
+            sh = gate_heads_forward(s_view, b32, hagg, heads, rope_s, out_t=sht if fused else None)   # (B, N, P)
         else:
             sh = gate_forward(s_view, b32, hagg, rope_s, out_t=sht if fused else None)   # (B, N, P)
         if want_sht and not fused:

@@ -216,24 +216,24 @@ def test_heads_validation_before_launch(lib):
     sh = ctypes.byref(_view(4096, 64 * 64, 64))
     hagg = ctypes.c_void_p(8192)
     # H must divide P
-    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 7, ys, None, hagg, 1, None, sh, None)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 7, ys, None, hagg, 1, None, sh, None, None)
     assert rc == _lib.POM_ERR_INVALID and b"divide P" in lib.pom_last_error()
     # groups must divide N
-    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 5, None, sh, None)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 5, None, sh, None, None)
     assert rc == _lib.POM_ERR_INVALID and b"groups" in lib.pom_last_error()
     # 1-D RoPE needs an even head count, 2-D a multiple of 4, tables wide enough
     pos = ctypes.c_void_p(512)
     r1 = _lib.PomRope(_lib.ROPE_1D, 1024, 2048, None, None, 4, 16, 0, pos.value, 1)
-    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 63, 7, ys, None, hagg, 1, ctypes.byref(r1), sh, None)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 63, 7, ys, None, hagg, 1, ctypes.byref(r1), sh, None, None)
     assert rc == _lib.POM_ERR_INVALID and b"even" in lib.pom_last_error()
     r1n = _lib.PomRope(_lib.ROPE_1D, 1024, 2048, None, None, 3, 16, 0, pos.value, 1)
-    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 1, ctypes.byref(r1n), sh, None)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 64, 8, ys, None, hagg, 1, ctypes.byref(r1n), sh, None, None)
     assert rc == _lib.POM_ERR_INVALID and b"narrower" in lib.pom_last_error()
     r2 = _lib.PomRope(_lib.ROPE_2D, 1024, 2048, 1024, 2048, 2, 16, 16, pos.value, 2)
-    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 60, 6, ys, None, hagg, 1, ctypes.byref(r2), sh, None)
+    rc = lib.pom_gate_heads_fwd(1, 1, 2, 64, 60, 6, ys, None, hagg, 1, ctypes.byref(r2), sh, None, None)
     assert rc == _lib.POM_ERR_INVALID and b"divisible by 4" in lib.pom_last_error()
     # parameter dtype and a short workspace
-    rc = lib.pom_gate_heads_fwd(1, 9, 2, 64, 64, 8, ys, None, hagg, 1, None, sh, None)
+    rc = lib.pom_gate_heads_fwd(1, 9, 2, 64, 64, 8, ys, None, hagg, 1, None, sh, None, None)
     assert rc == _lib.POM_ERR_INVALID and b"param_dtype" in lib.pom_last_error()
     need = lib.pom_gate_heads_workspace_size(1, 2, 64, 64, 8, 1)
     assert need > 0 and lib.pom_gate_heads_workspace_size(1, 2, 64, 64, 7, 1) == 0

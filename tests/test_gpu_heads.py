@@ -60,10 +60,29 @@ def _case(device, B, N, P, H, G, dtype, rope=None, bias=True, strided=True, seed
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,N,P,H,G", [(2, 64, 64, 4, 1), (2, 128, 576, 16, 1), (2, 96, 96, 8, 3),
                                        (2, 40, 48, 4, 40), (1, 33, 24, 3, 1), (2, 50, 36, 4, 1),
-                                       (2, 30, 60, 6, 5)])
+                                       (2, 30, 60, 6, 5), (2, 256, 128, 8, 2), (2, 100, 40, 5, 1),
+                                       (1, 64, 200, 25, 64)])
 def test_heads_plain(device, B, N, P, H, G, dtype):
-    # head_dim 16, 36, 12, 12, 8, 9 (scalar chunks), 10 (pairs)
+    # tile path: 64-token groups or single-token groups with P % 8 == 0 (head_dim 16, 36, 12, 16,
+    # 8 — 64-channel tiles touching up to 9 heads); general path: 32-token frames, 33 tokens,
+    # head_dim 9 (scalar chunks) and 10 (pairs), P = 40 in a 100-token row
     _case(device, B, N, P, H, G, dtype)
+
+
+@pytest.mark.parametrize("N,P,H", [(128, 576, 16), (64, 200, 25), (40, 64, 8)])
+def test_heads_channel_major_copy(device, N, P, H):
+    """sh and its channel-major copy (P, B*N) from one launch (bf16); shapes the
+    kernels do not build the copy for fall back to the transpose kernel."""
+    g = torch.Generator().manual_seed(9)
+    B = 2
+    ys = (torch.randn(B, N, H, generator=g) * 2).to(device, torch.bfloat16)
+    hagg = torch.randn(B, 1, P, generator=g).to(device, torch.bfloat16)
+    bias = torch.randn(H, generator=g).to(device, torch.bfloat16)
+    sht = torch.full((P, B * N), float("nan"), device=device, dtype=torch.bfloat16)
+    sh = ops.gate_heads_forward(ys, bias, hagg, H, None, out_t=sht)
+    ref = ops.gate_heads_forward(ys, bias, hagg, H, None)
+    assert torch.equal(sh, ref)
+    assert torch.equal(sht, sh.reshape(B * N, P).t())
 
 
 def test_heads_no_bias_contiguous(device):
