@@ -383,18 +383,24 @@ def _pmc_per_kernel(db: str, counter: str):
 COPY_CALIB_MIB = 144   # pmc_summary expects the calibration run made with --copy-calib 144
 
 
+def _is_gate_bwd(name: str) -> bool:
+    """The gate backward's main kernel (full-width or per-head)."""
+    return any(k in name for k in ("gate_bwd_kernel", "heads_bwd_tile", "heads_bwd_token_kernel"))
+
+
 def _gemm_dispatches(db: str):
     """Dispatch id and library kernel name of each projection GEMM of the last
     complete fwd+bwd step, from the dispatch order: qc_fwd precedes
-    agg_fwd_chunk, ag_fwd follows gate_fwd, ag_dgrad and ag_wgrad precede
-    gate_bwd, qc_dgrad and qc_wgrad follow coeff_grad_finalize.  (One library
+    agg_fwd_chunk, ag_fwd follows the gate forward, ag_dgrad and ag_wgrad
+    precede the gate backward, qc_dgrad and qc_wgrad follow
+    coeff_grad_finalize.  (One library
     kernel can serve several GEMMs, so names alone do not identify them.)"""
     import sqlite3
     c = sqlite3.connect(db)
     seq = [(r[0], r[1]) for r in c.execute("select dispatch_id, kernel_name from counters_collection "
                                            "group by dispatch_id order by dispatch_id")]
     order = ["gemm_qc_fwd", "gemm_ag_fwd", "gemm_ag_dgrad", "gemm_ag_wgrad", "gemm_qc_dgrad", "gemm_qc_wgrad"]
-    gb = max(i for i, (_, n) in enumerate(seq) if "gate_bwd_kernel" in n)
+    gb = max(i for i, (_, n) in enumerate(seq) if _is_gate_bwd(n))
     af = max(i for i, (_, n) in enumerate(seq[:gb]) if "agg_fwd_chunk" in n)
     pre = [d for d in seq[:af] if "Cijk" in d[1]]
     gemms = [pre[-1]] + [d for d in seq[af:] if "Cijk" in d[1]][:5]
@@ -467,7 +473,7 @@ def trace_summary(trace_dir):
     afs = [i for i, n in enumerate(seq) if "agg_fwd_chunk" in n]
     for k, af in enumerate(afs):
         end = afs[k + 1] if k + 1 < len(afs) else len(seq)
-        if not any("gate_bwd_kernel" in n for n in seq[af:end]):
+        if not any(_is_gate_bwd(n) for n in seq[af:end]):
             continue   # a forward-only pass
         pre = [i for i in range(af) if "Cijk" in seq[i]]
         idx = [pre[-1]] + [i for i in range(af, end) if "Cijk" in seq[i]][:5]
