@@ -256,10 +256,17 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
   map.init(active ? vcol : 0, p.P);
 
   float c[CPT2][KM];
+  {
+    float flat[CPT2 * KM];
+    param_gather<CPT2 * KM>(p.coeff, [&](int q) {
+      const int j = q % KM;
+      return map.chan(q / KM) * p.K + (j < p.K ? j : p.K - 1);
+    }, flat);
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i)
+    for (int i = 0; i < CPT2; ++i)
 #pragma unroll
-    for (int j = 0; j < KM; ++j) c[i][j] = (active && j < p.K) ? param_get(p.coeff, map.chan(i) * p.K + j) : 0.0f;
+      for (int j = 0; j < KM; ++j) c[i][j] = (active && j < p.K) ? flat[i * KM + j] : 0.0f;
+  }
 
   float acc[CPT2];
 #pragma unroll
@@ -447,25 +454,35 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
   float d[CPT2][KM], g[CPT2][KM], w[CPT2];
   float cntv = 1.0f;
   if constexpr (MASKED) cntv = p.count_in[b];
+  {
+    float flat[CPT2 * KM];
+    param_gather<CPT2 * KM>(p.coeff, [&](int q) {
+      const int j = q % KM;
+      return map.chan(q / KM) * p.K + (j < p.K ? j : p.K - 1);
+    }, flat);
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i) {
-    const int64_t ch = map.chan(i);
+    for (int i = 0; i < CPT2; ++i)
 #pragma unroll
-    for (int j = 0; j < KM; ++j) {
-      d[i][j] = (active && j < p.K) ? param_get(p.coeff, ch * p.K + j) * (float)(j + 1) : 0.0f;
-      g[i][j] = 0.0f;
-    }
-    float wi = 0.0f;
-    if (active) {
-      if constexpr (MASKED) {
-        wi = cntv != 0.0f ? p.go[b * p.P + ch] / cntv : 0.0f;
-      } else if (p.wf) {
-        wi = p.wf[(b * p.g.F + f) * p.P + ch];
-      } else {
-        wi = (p.go[b * p.P + ch] / ((float)p.n_past + 1.0f)) / (float)p.g.L;
+      for (int j = 0; j < KM; ++j) {
+        d[i][j] = (active && j < p.K) ? flat[i * KM + j] * (float)(j + 1) : 0.0f;
+        g[i][j] = 0.0f;
       }
+  }
+  {
+    // all weight loads first (one source for the whole lane), then the
+    // per-mode arithmetic
+    const float* wsrc = (!MASKED && p.wf) ? p.wf + (b * p.g.F + f) * p.P : p.go + b * p.P;
+    float raw[CPT2];
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) raw[i] = wsrc[map.chan(i)];
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) {
+      float wi;
+      if constexpr (MASKED) wi = cntv != 0.0f ? raw[i] / cntv : 0.0f;
+      else if (p.wf) wi = raw[i];
+      else wi = (raw[i] / ((float)p.n_past + 1.0f)) / (float)p.g.L;
+      w[i] = active ? wi : 0.0f;
     }
-    w[i] = wi;
   }
   float w01[CPT2];
 #pragma unroll

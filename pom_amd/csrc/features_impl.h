@@ -21,10 +21,17 @@ __global__ void __launch_bounds__(kThreads) features_fwd_kernel(const FeatParams
   const int64_t rbeg = chunk * p.RC, rend = rbeg + p.RC < p.N ? rbeg + p.RC : p.N;
   const int64_t c0 = j * V;
   float c[V][KM];
+  {
+    float flat[V * KM];
+    param_gather<V * KM>(p.coeff, [&](int q) {
+      const int k = q % KM;
+      return (c0 + q / KM) * p.K + (k < p.K ? k : p.K - 1);
+    }, flat);
 #pragma unroll
-  for (int v = 0; v < V; ++v)
+    for (int v = 0; v < V; ++v)
 #pragma unroll
-    for (int k = 0; k < KM; ++k) c[v][k] = k < p.K ? param_get(p.coeff, (c0 + v) * p.K + k) : 0.0f;
+      for (int k = 0; k < KM; ++k) c[v][k] = k < p.K ? flat[v * KM + k] : 0.0f;
+  }
   const T* xb = reinterpret_cast<const T*>(p.x) + b * p.sxb + c0;
   T* ob = reinterpret_cast<T*>(p.out) + b * p.sob + c0;
   for (int64_t n = rbeg; n < rend; ++n) {
@@ -44,13 +51,20 @@ __global__ void __launch_bounds__(kThreads) features_bwd_kernel(const FeatParams
   const int64_t rbeg = chunk * p.RC, rend = rbeg + p.RC < p.N ? rbeg + p.RC : p.N;
   const int64_t c0 = j * V;
   float d[V][KM], g[V][KM];
+  {
+    float flat[V * KM];
+    param_gather<V * KM>(p.coeff, [&](int q) {
+      const int k = q % KM;
+      return (c0 + q / KM) * p.K + (k < p.K ? k : p.K - 1);
+    }, flat);
 #pragma unroll
-  for (int v = 0; v < V; ++v)
+    for (int v = 0; v < V; ++v)
 #pragma unroll
-    for (int k = 0; k < KM; ++k) {
-      d[v][k] = k < p.K ? param_get(p.coeff, (c0 + v) * p.K + k) * (float)(k + 1) : 0.0f;
-      g[v][k] = 0.0f;
-    }
+      for (int k = 0; k < KM; ++k) {
+        d[v][k] = k < p.K ? flat[v * KM + k] * (float)(k + 1) : 0.0f;
+        g[v][k] = 0.0f;
+      }
+  }
   const T* xb = reinterpret_cast<const T*>(p.x) + b * p.sxb + c0;
   const T* gb = reinterpret_cast<const T*>(p.go) + b * p.sgob + c0;
   T* dxb = reinterpret_cast<T*>(p.gx) + b * p.sgxb + c0;

@@ -40,8 +40,12 @@ __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, 
   const int64_t ngroups = per_token ? p.N : p.g.F;
 
   float bias[CPT2], hv[CPT2];
+  if (p.bias.ptr) {
+    param_gather<CPT2>(p.bias, [&](int i) { return map.chan(i); }, bias);
+  } else {
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i) bias[i] = p.bias.ptr ? param_get(p.bias, map.chan(i)) : 0.0f;
+    for (int i = 0; i < CPT2; ++i) bias[i] = 0.0f;
+  }
   const T* hb = reinterpret_cast<const T*>(p.hagg) + b * ngroups * p.P;
   if (!per_token) {
     Pack<T, CPT> h1, h2;
@@ -152,12 +156,23 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
 
   float bias[CPT2], hv[CPT2], dh[CPT2], db[CPT2];
   const T* hb = reinterpret_cast<const T*>(p.hagg) + b * ngroups * p.P;
+  if (p.bias.ptr) {
+    param_gather<CPT2>(p.bias, [&](int i) { return map.chan(i); }, bias);
+  } else {
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i) {
-    bias[i] = (active && p.bias.ptr) ? param_get(p.bias, map.chan(i)) : 0.0f;
-    hv[i] = (active && !per_token) ? to_f32<T>(hb[f * p.P + map.chan(i)]) : 0.0f;
-    dh[i] = 0.0f;
-    db[i] = 0.0f;
+    for (int i = 0; i < CPT2; ++i) bias[i] = 0.0f;
+  }
+  {
+    T raw[CPT2];
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) raw[i] = hb[(per_token ? 0 : f) * p.P + map.chan(i)];
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) {
+      bias[i] = active ? bias[i] : 0.0f;
+      hv[i] = (active && !per_token) ? to_f32<T>(raw[i]) : 0.0f;
+      dh[i] = 0.0f;
+      db[i] = 0.0f;
+    }
   }
 
   const T* yb = reinterpret_cast<const T*>(p.ys) + b * p.ysb;

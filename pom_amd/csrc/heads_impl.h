@@ -61,20 +61,22 @@ __device__ __forceinline__ void head_pair(int64_t H, int64_t h, int& blk, int64_
 // the H gate channels).
 template <typename T, int MODE>
 __device__ __forceinline__ float head_gate(const HeadsParams& p, const T* __restrict__ yrow, int64_t n, int64_t h) {
-  auto sg = [&](int64_t k) {
-    const float z = to_f32<T>(yrow[k]) + (p.bias.ptr ? param_get(p.bias, k) : 0.0f);
-    return hsig(z);
-  };
-  const float s = sg(h);
+  // every load (y_s and bias of the head and its rotation partner, the table
+  // entries) is issued before any of them is used
+  int64_t k[2] = {h, h};
+  int blk = 0, table = 0;
+  int64_t col = 0;
+  if constexpr (MODE != MODE_PLAIN) head_pair<MODE>(p.H, h, blk, col, k[1], table);
+  const T y0 = yrow[k[0]], y1 = yrow[k[1]];
+  float bv[2] = {0.0f, 0.0f};
+  if (p.bias.ptr) param_gather<2>(p.bias, [&](int q) { return k[q]; }, bv);
+  const float s = hsig(to_f32<T>(y0) + bv[0]);
   if constexpr (MODE == MODE_PLAIN) {
     return s;
   } else {
-    int blk, table;
-    int64_t col, partner;
-    head_pair<MODE>(p.H, h, blk, col, partner, table);
-    const float sp = sg(partner);
     float cs, sn;
     table_cs(p.rope, table, n, col, cs, sn);
+    const float sp = hsig(to_f32<T>(y1) + bv[1]);
     return blk ? s * cs + sp * sn : s * cs - sp * sn;
   }
 }

@@ -19,6 +19,26 @@ __device__ __forceinline__ float param_get(const ParamIn& a, int64_t i) {
   if (a.dt == DT_F16) return to_f32<__half>(static_cast<const __half*>(a.ptr)[i]);
   return static_cast<const float*>(a.ptr)[i];
 }
+// out[q] = a[idx(q)] in fp32 for q < N, with one dtype dispatch around all the
+// loads: a dispatch per element (param_get) puts each load's wait inside its
+// branch, so the loads of a lane run one after another.  idx(q) must be a valid
+// element index for every q.
+template <int N, typename Idx>
+__device__ __forceinline__ void param_gather(const ParamIn& a, Idx&& idx, float (&out)[N]) {
+  auto run = [&](auto tag) {
+    using PT = decltype(tag);
+    const PT* s = static_cast<const PT*>(a.ptr);
+    PT raw[N];
+#pragma unroll
+    for (int q = 0; q < N; ++q) raw[q] = s[idx(q)];
+#pragma unroll
+    for (int q = 0; q < N; ++q) out[q] = to_f32<PT>(raw[q]);
+  };
+  if (a.dt == DT_BF16) run(__hip_bfloat16{});
+  else if (a.dt == DT_F16) run(__half{});
+  else run(float{});
+}
+
 __device__ __forceinline__ void param_set(const ParamOut& a, int64_t i, float v) {
   if (a.dt == DT_BF16) static_cast<__hip_bfloat16*>(a.ptr)[i] = from_f32<__hip_bfloat16>(v);
   else if (a.dt == DT_F16) static_cast<__half*>(a.ptr)[i] = from_f32<__half>(v);

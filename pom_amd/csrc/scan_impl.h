@@ -58,11 +58,18 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanParams p) 
 
   float c[CPT2][KM], acc[CPT2];
   const float* pre = p.csum + (b * p.nch + chunk) * p.P;
+  {
+    float flat[CPT2 * KM];
+    param_gather<CPT2 * KM>(p.coeff, [&](int q) {
+      const int j = q % KM;
+      return map.chan(q / KM) * p.K + (j < p.K ? j : p.K - 1);
+    }, flat);
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i) {
+    for (int i = 0; i < CPT2; ++i) {
 #pragma unroll
-    for (int j = 0; j < KM; ++j) c[i][j] = j < p.K ? param_get(p.coeff, map.chan(i) * p.K + j) : 0.0f;
-    acc[i] = pre[map.chan(i)];
+      for (int j = 0; j < KM; ++j) c[i][j] = j < p.K ? flat[i * KM + j] : 0.0f;
+      acc[i] = pre[map.chan(i)];
+    }
   }
   const int64_t rbeg = chunk * p.RC;
   const int64_t rend = rbeg + p.RC < p.N ? rbeg + p.RC : p.N;
@@ -146,14 +153,21 @@ __global__ void __launch_bounds__(kThreads) scan_bwd_kernel(const ScanParams p) 
 
   float c[CPT2][KM], g[CPT2][KM], sw[CPT2];
   const float* suf = p.csum + (b * p.nch + chunk) * p.P;
+  {
+    float flat[CPT2 * KM];
+    param_gather<CPT2 * KM>(p.coeff, [&](int q) {
+      const int j = q % KM;
+      return map.chan(q / KM) * p.K + (j < p.K ? j : p.K - 1);
+    }, flat);
 #pragma unroll
-  for (int i = 0; i < CPT2; ++i) {
+    for (int i = 0; i < CPT2; ++i) {
 #pragma unroll
-    for (int j = 0; j < KM; ++j) {
-      c[i][j] = j < p.K ? param_get(p.coeff, map.chan(i) * p.K + j) : 0.0f;
-      g[i][j] = 0.0f;
+      for (int j = 0; j < KM; ++j) {
+        c[i][j] = j < p.K ? flat[i * KM + j] : 0.0f;
+        g[i][j] = 0.0f;
+      }
+      sw[i] = suf[map.chan(i)];
     }
-    sw[i] = suf[map.chan(i)];
   }
   const int64_t rbeg = chunk * p.RC;
   const int64_t rend = rbeg + p.RC < p.N ? rbeg + p.RC : p.N;
