@@ -135,6 +135,9 @@ def kernel_work(cfg, extra):
     """name -> (bound, algorithmic bytes or flops per launch, what one unit is)."""
     B, N, D, K, E = cfg["B"], cfg["N"], cfg["D"], cfg["K"], cfg["E"]
     T, P, e = B * N, E * D, 2
+    H = cfg.get("heads", 1)
+    S = H if H > 1 else P   # gate columns of Y: one per head, or one per channel
+    Q = P + S               # useful projection width (padding columns are not counted)
     G = {"mean": 1, "masked": 1, "block": N // cfg.get("frame_len", N), "rope2d": 1}[cfg["variant"]]
     read_tok = T
     if cfg["variant"] == "masked":
@@ -148,30 +151,31 @@ def kernel_work(cfg, extra):
     from pom_amd import ops
     cm = T * P * e if (ops._NT_GEMMS and ops._NT_COPIES == "fused") else 0
     w = {
-        "gemm_qc_fwd": ("mfma", 2.0 * T * D * 2 * P),
+        "gemm_qc_fwd": ("mfma", 2.0 * T * D * Q),
         "gemm_ag_fwd": ("mfma", 2.0 * T * P * D),
         "gemm_ag_dgrad": ("mfma", 2.0 * T * D * P),
         "gemm_ag_wgrad": ("mfma", 2.0 * T * D * P),
-        "gemm_qc_dgrad": ("mfma", 2.0 * T * 2 * P * D),
-        "gemm_qc_wgrad": ("mfma", 2.0 * T * 2 * P * D),
+        "gemm_qc_dgrad": ("mfma", 2.0 * T * Q * D),
+        "gemm_qc_wgrad": ("mfma", 2.0 * T * Q * D),
         # x read (valid tokens only when masked) + aggregate written
         "agg_fwd": ("hbm", float(read_tok * P * e + agg_out + mask_b + rope_tab)),
         # x read for valid tokens, grad_x (and its channel-major copy) written for every token,
         # fp32 upstream grad read
         "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + cm + B * G * P * 4 + mask_b)),
-        # y_s read, sh (and sh^T) written
-        "gate_fwd": ("hbm", float(2 * T * P * e + cm + B * G * P * 4)),
+        # y_s read, sh (and sh^T) written, aggregate read
+        "gate_fwd": ("hbm", float(2 * T * P * e + cm + B * G * P * e)),
         # y_s and dsh read, dy_s (and its channel-major copy) written
         "gate_bwd": ("hbm", float(3 * T * P * e + cm + B * G * P * 4)),
-        # per-head gate: sh written (y_s and hagg are H / P wide per token / row)
-        "gate_heads_fwd": ("hbm", float(T * P * e + T * cfg.get("heads", 1) * e + B * G * P * e)),
+        # per-head gate: sh (and sh^T) written (y_s and hagg are H / P wide per token / row)
+        "gate_heads_fwd": ("hbm", float(T * P * e + cm + T * H * e + B * G * P * e)),
         # dsh read once, y_s read, dy_s written, fp32 dhagg written
-        "gate_heads_bwd": ("hbm", float(T * P * e + 2 * T * cfg.get("heads", 1) * e + B * G * P * 4)),
+        "gate_heads_bwd": ("hbm", float(T * P * e + 2 * T * H * e + B * G * P * 4)),
         # operand-layout transposes for the backward GEMMs: read + write once
         "transpose_x": ("hbm", float(2 * T * D * e)),
         "transpose_sh": ("hbm", float(2 * T * P * e)),
         "transpose_g": ("hbm", float(2 * T * D * e)),
-        "transpose_dy": ("hbm", float(2 * T * 2 * P * e)),
+        # all of dY, or only its gate part when the streaming kernels write the rest
+        "transpose_dy": ("hbm", float(2 * T * (S if cm else Q) * e)),
         "transpose_w": ("hbm", float(2 * 2 * P * D * e)),   # W_qc or W_ag: counted as the larger
     }
     return w

@@ -375,6 +375,13 @@ int64_t heads_nhm(int64_t P, int64_t H) {
   return n < H ? n : H;
 }
 
+// Token tiles per backward workgroup: 4 when every walk stays inside one group
+// (single-token groups, or groups a multiple of 4 tiles long), else 1.
+int heads_tpw(int64_t N, int64_t L) {
+  (void)N;
+  return (L == 1 || L % (4 * kHeadTile) == 0) ? 4 : 1;
+}
+
 size_t heads_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups) {
   int64_t nch = 1, tok_wgs = 1;
   for (int V : {1, 2, 4, 8}) {   // every chunk width the call may choose
@@ -432,7 +439,8 @@ int setup_heads(pom::HeadsParams& p, int dtype, int param_dtype, int64_t B, int6
   for (const pom_view* v : views)
     tile = tile && aligned(v->data, 16) && v->stride_b % 8 == 0 && v->stride_n % 8 == 0;
   p.tile = tile ? 1 : 0;
-  p.ntt = cdiv(N, kHeadTile);
+  p.tpw = heads_tpw(N, p.L);
+  p.ntt = cdiv(N, kHeadTile * p.tpw);
   p.nhm = heads_nhm(P, H);
   return POM_OK;
 }

@@ -319,73 +319,88 @@ __global__ void __launch_bounds__(kThreads) heads_bwd_tile(const HeadsParams p) 
   __shared__ float red[4 * kCT];
   __shared__ int hidx[kCT];
   const int tid = threadIdx.x;
-  const int64_t b = blockIdx.z, n0 = (int64_t)blockIdx.y * kTT, c0 = (int64_t)blockIdx.x * kCT;
-  const int nt = (int)(p.N - n0 < kTT ? p.N - n0 : kTT), nc = (int)(p.P - c0 < kCT ? p.P - c0 : kCT);
+  // this workgroup walks p.tpw consecutive token tiles of one batch row (inside one group)
+  const int64_t b = blockIdx.z, c0 = (int64_t)blockIdx.x * kCT;
+  const int64_t n_first = (int64_t)blockIdx.y * p.tpw * kTT;
+  const int nc = (int)(p.P - c0 < kCT ? p.P - c0 : kCT);
   const bool per_token = p.L == 1;
   const int cj = nc / 8;
   const T* gb = reinterpret_cast<const T*>(p.dsh) + b * p.dsb + c0;
   const T* hb = reinterpret_cast<const T*>(p.hagg) + b * p.G * p.P + c0;
-  // this thread's two chunks (t, j) = (i >> 3, i & 7), i = tid and tid + 256:
-  // dsh and hagg are loaded before the gate values are formed, so the memory
-  // latencies overlap
+  const int64_t nct = (p.P + kCT - 1) / kCT;
   constexpr int R = kTT * 8 / kThreads;
   Pack<T, 8> gp[R], hp[R];
+  // loads of one tile's dsh (and hagg) chunks: (t, j) = (i >> 3, i & 7), i = tid + r * 256
+  auto load_tile = [&](int64_t n0, int nt) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
-    if (t < nt && j < cj) {
-      gp[r].load(gb + (n0 + t) * p.dsn + j * 8);
-      hp[r].load(hb + (per_token ? n0 + t : n0 / p.L) * p.P + j * 8);
+    for (int r = 0; r < R; ++r) {
+      const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
+      if (t < nt && j < cj) {
+        gp[r].load(gb + (n0 + t) * p.dsn + j * 8);
+        hp[r].load(hb + (per_token ? n0 + t : n0 / p.L) * p.P + j * 8);
+      }
     }
-  }
-  int64_t h0;
-  int nh;
-  tile_gates<T, MODE>(p, b, n0, c0, nt, nc, h0, nh, hidx, gs);
-  __syncthreads();
+  };
+  const int ntiles = (int)((p.N - n_first + kTT - 1) / kTT) < p.tpw ? (int)((p.N - n_first + kTT - 1) / kTT) : p.tpw;
+  float acc = 0.0f;   // this thread's quarter sum of s' * dsh (channel tid & 63), over the walk
+  load_tile(n_first, (int)(p.N - n_first < kTT ? p.N - n_first : kTT));
+  for (int k = 0; k < ntiles; ++k) {
+    const int64_t n0 = n_first + (int64_t)k * kTT;
+    const int nt = (int)(p.N - n0 < kTT ? p.N - n0 : kTT);
+    int64_t h0;
+    int nh;
+    __syncthreads();   // the previous tile's readers of gs / cd / pr are done
+    tile_gates<T, MODE>(p, b, n0, c0, nt, nc, h0, nh, hidx, gs);
+    __syncthreads();
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
-    if (t >= nt || j >= cj) continue;
-    const int cc = j * 8, ha = hidx[cc];
-    float pa = 0.0f, pb = 0.0f, o[8];
+    for (int r = 0; r < R; ++r) {
+      const int i = tid + r * kThreads, t = i >> 3, j = i & 7;
+      if (t >= nt || j >= cj) continue;
+      const int cc = j * 8, ha = hidx[cc];
+      float pa = 0.0f, pb = 0.0f, o[8];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      const int hv = hidx[cc + v];
-      const float g = gp[r].get(v), d = g * hp[r].get(v);
-      if (hv == ha) pa += d;
-      else pb += d;
-      o[v] = gs[t * kGM + hv] * g;
-    }
-    cd[i * 2] = pa;
-    cd[i * 2 + 1] = pb;
-    if (per_token) {
-      store_f32<8>(p.dhagg + (b * p.G + n0 + t) * p.P + c0 + cc, o);
-    } else {
+      for (int v = 0; v < 8; ++v) {
+        const int hv = hidx[cc + v];
+        const float g = gp[r].get(v), d = g * hp[r].get(v);
+        if (hv == ha) pa += d;
+        else pb += d;
+        o[v] = gs[t * kGM + hv] * g;
+      }
+      cd[i * 2] = pa;
+      cd[i * 2 + 1] = pb;
+      if (per_token) {
+        store_f32<8>(p.dhagg + (b * p.G + n0 + t) * p.P + c0 + cc, o);
+      } else {
 #pragma unroll
-      for (int v = 0; v < 8; ++v) pr[t * DP + cc + v] = o[v];
+        for (int v = 0; v < 8; ++v) pr[t * DP + cc + v] = o[v];
+      }
     }
-  }
-  __syncthreads();
-  // per-head dot products of the tile's channels: d s'[t][hi] partial
-  const int64_t nct = (p.P + kCT - 1) / kCT;
-  for (int i = tid; i < nt * nh; i += kThreads) {
-    const int t = i / nh, hi = i - t * nh;
-    float d = 0.0f;
-    for (int j = 0; j < cj; ++j) {
-      const int ha = hidx[j * 8], hz = hidx[j * 8 + 7];
-      d += (ha == hi ? cd[(t * 8 + j) * 2] : 0.0f) + (hz == hi && hz != ha ? cd[(t * 8 + j) * 2 + 1] : 0.0f);
+    // the next tile's loads go out before this tile's reductions
+    if (k + 1 < ntiles) {
+      const int64_t n1 = n0 + kTT;
+      load_tile(n1, (int)(p.N - n1 < kTT ? p.N - n1 : kTT));
     }
-    p.dpart[((b * p.N + n0 + t) * nct + blockIdx.x) * p.nhm + hi] = d;
+    __syncthreads();
+    for (int i = tid; i < nt * nh; i += kThreads) {
+      const int t = i / nh, hi = i - t * nh;
+      float d = 0.0f;
+      for (int j = 0; j < cj; ++j) {
+        const int ha = hidx[j * 8], hz = hidx[j * 8 + 7];
+        d += (ha == hi ? cd[(t * 8 + j) * 2] : 0.0f) + (hz == hi && hz != ha ? cd[(t * 8 + j) * 2 + 1] : 0.0f);
+      }
+      p.dpart[((b * p.N + n0 + t) * nct + blockIdx.x) * p.nhm + hi] = d;
+    }
+    if (!per_token) {
+      const int c = tid & (kCT - 1), q = tid >> 6;
+      if (c < nc) {
+        const int te = (q + 1) * (kTT / 4) < nt ? (q + 1) * (kTT / 4) : nt;
+        for (int t = q * (kTT / 4); t < te; ++t) acc += pr[t * DP + c];
+      }
+    }
   }
   if (!per_token) {
-    // the tile's sum over its tokens: four token quarters, then a fixed sum
-    const int c = tid & (kCT - 1), q = tid >> 6;
-    float a = 0.0f;
-    if (c < nc) {
-      const int te = (q + 1) * (kTT / 4) < nt ? (q + 1) * (kTT / 4) : nt;
-      for (int t = q * (kTT / 4); t < te; ++t) a += pr[t * DP + c];
-    }
-    red[q * kCT + c] = a;
+    // the walk's sum over its tokens: four token quarters, then a fixed sum
+    red[tid] = acc;
     __syncthreads();
     if (tid < nc)
       p.part_h[(b * p.ntt + blockIdx.y) * p.P + c0 + tid] =
@@ -393,8 +408,6 @@ __global__ void __launch_bounds__(kThreads) heads_bwd_tile(const HeadsParams p) 
   }
 }
 
-// Per (token, head): d s' from the channel-tile partials, R^T, hardsigmoid',
-// dY_s; dz summed per head over the workgroup's kTT tokens (bias partial).
 constexpr int kDzT = 16;   // tokens per workgroup of the dz kernel (= rows per bias partial)
 
 template <typename T, int MODE>
@@ -447,7 +460,7 @@ static __global__ void __launch_bounds__(kThreads) heads_tile_finalize(const Hea
   const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (p.L > 1 && idx < p.B * p.G * p.P) {
     const int64_t c = idx % p.P, bg = idx / p.P, b = bg / p.G, g = bg - b * p.G;
-    const int64_t per = p.L / kTT;
+    const int64_t per = p.L / (kTT * p.tpw);   // walks per group
     const float* src = p.part_h + (b * p.ntt + g * per) * p.P + c;
     float s = 0.0f;
     int64_t k = 0;
@@ -492,7 +505,7 @@ hipError_t heads_tile_fwd_m(const HeadsParams& p, hipStream_t st) {
 
 template <typename T, int MODE>
 hipError_t heads_tile_bwd_m(const HeadsParams& p, hipStream_t st) {
-  const dim3 grid((unsigned)((p.P + kCT - 1) / kCT), (unsigned)((p.N + kTT - 1) / kTT), (unsigned)p.B);
+  const dim3 grid((unsigned)((p.P + kCT - 1) / kCT), (unsigned)p.ntt, (unsigned)p.B);
   hipLaunchKernelGGL((heads_bwd_tile<T, MODE>), grid, dim3(kThreads), 0, st, p);
   if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
   const int64_t nb = (p.B * p.N + kDzT - 1) / kDzT;

@@ -239,11 +239,12 @@ struct HeadsParams {
   int64_t RC = 1, cpf = 1, nch = 1;   // aggregate-gradient chunks: cpf chunks of RC rows per group
   float* sgate = nullptr;         // (B, N, H) fp32 rotated gate values
   float* part_b = nullptr;        // (tok_wgs, H)
-  float* part_h = nullptr;        // (B, nch, P) | tile path: (B, ntt, P) token-tile partials
+  float* part_h = nullptr;        // (B, nch, P) | tile path: (B, ntt, P) per-walk partials
 
   // tile path (64 tokens x 64 channels per workgroup)
   int tile = 0;
-  int64_t ntt = 1;                // token tiles per batch row
+  int tpw = 1;                    // token tiles per backward workgroup (a walk stays inside one group)
+  int64_t ntt = 1;                // backward walks per batch row = cdiv(N, 64 * tpw)
   int64_t nhm = 1;                // heads a channel tile can touch (dot-partial stride)
   float* dpart = nullptr;         // (B * N, channel tiles, nhm) per-head dot partials
   float* dzbuf = nullptr;         // (cdiv(B * N, 16), H) fp32 dz sums per 16-token group

@@ -98,6 +98,7 @@ def _check_degree(k: int) -> None:
 
 _f32_cache: dict = {}
 _wt_cache: dict = {}
+_pad_cache: dict = {}
 
 
 def _param(t: torch.Tensor) -> torch.Tensor:
@@ -132,6 +133,7 @@ def invalidate_derived() -> None:
     weights), as an optimizer update of all parameters would."""
     _f32_cache.clear()
     _wt_cache.clear()
+    _pad_cache.clear()
 
 
 def _transpose_into(src: torch.Tensor, dst: torch.Tensor, name: str) -> None:
@@ -164,6 +166,28 @@ def _with_copy(call, out_t, src_rows: torch.Tensor, name: str, what: str, B: int
 def _weight_t(w: torch.Tensor) -> torch.Tensor:
     """Transposed copy of a projection weight, cached per weight version."""
     return _derived(_wt_cache, w, lambda u: transpose(u.detach(), "transpose_w"))
+
+
+def _padded_width(p: int, s: int) -> int:
+    """Projection width P + S rounded up to 64 columns: 128-byte-aligned rows of
+    Y / dY for the streaming kernels and an aligned GEMM dimension (per-head
+    gating makes P + S = P + n_sel_heads, which is rarely aligned)."""
+    return (p + s + 63) // 64 * 64
+
+
+def _qc_weight(w: torch.Tensor, dt: torch.dtype, rows: int) -> torch.Tensor:
+    """W_qc in dtype dt with zero rows appended up to ``rows`` (the padded
+    projection width), cached per weight version."""
+    def make(u):
+        u = u.detach().to(dt)
+        if u.shape[0] == rows:
+            return u
+        out = torch.zeros(rows, u.shape[1], dtype=dt, device=u.device)
+        out[:u.shape[0]] = u
+        return out
+    if w.dtype == dt and w.shape[0] == rows:
+        return w
+    return _derived(_pad_cache, w, make)
 
 
 def _coeff_param(coeff: torch.Tensor, p: int, k: int) -> torch.Tensor:
@@ -598,6 +622,7 @@ class _PoMLayer(torch.autograd.Function):
         B, N, D = x.shape
         P = coeff.shape[0]
         S = heads if heads > 1 else P
+        W = _padded_width(P, S)   # Y's row width (zero columns past P + S)
         T = B * N
         dt = x.dtype
         dev = x.device
@@ -612,11 +637,11 @@ class _PoMLayer(torch.autograd.Function):
             side.wait_stream(cur)
             with torch.cuda.stream(side):
                 xt = transpose(x2, "transpose_x")                  # (D, T), overlaps qc_fwd
-        wq = w_qc if w_qc.dtype == dt else w_qc.to(dt)
+        wq = _qc_weight(w_qc, dt, W)                                # (W, D), zero rows past P + S
         with _Span("gemm_qc_fwd"), tuned_gemms():
-            y = torch.mm(x2, wq.t())                                # (T, P+S)
-        y3 = y.view(B, N, P + S)
-        h_view, s_view = y3[..., :P], y3[..., P:]
+            y = torch.mm(x2, wq.t())                                # (T, W)
+        y3 = y.view(B, N, W)
+        h_view, s_view = y3[..., :P], y3[..., P:P + S]
         c32 = _coeff_param(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
         b32 = _param(se_bias)
@@ -664,6 +689,7 @@ class _PoMLayer(torch.autograd.Function):
             grad_out = torch.zeros(B, N, D, dtype=dt, device=dev)
         P = c32.shape[0]
         S = heads if heads > 1 else P
+        W = _padded_width(P, S)
         T = B * N
         need_x, need_wq, need_wa = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[4]
         nt_a = xt is not None or sht is not None   # token-contiguous weight gradients
@@ -700,20 +726,23 @@ class _PoMLayer(torch.autograd.Function):
                 with _Span("gemm_ag_wgrad"), tuned_gemms():
                     dw_ag = torch.mm(g2.t(), sh.view(T, P))         # (D, P)
         db_ag = g2.float().sum(0) if has_bias else None
-        y3 = y.view(B, N, P + S)
-        dy = torch.empty(T, P + S, dtype=dt, device=dev)
-        dy3 = dy.view(B, N, P + S)
+        y3 = y.view(B, N, W)
+        dy = torch.empty(T, W, dtype=dt, device=dev)
+        dy3 = dy.view(B, N, W)
+        if W > P + S:
+            dy[:, P + S:].zero_()   # the padding columns meet W_qc's zero rows in dx = dY W_qc
         want_dyt = need_wq and xt is not None
         fused = want_dyt and _NT_COPIES == "fused"
-        dyt = torch.empty(P + S, T, dtype=dt, device=dev) if fused else None
+        dyt = torch.empty(W, T, dtype=dt, device=dev) if fused else None
         if heads > 1:
-            _, dh, dbias = gate_heads_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), heads, rope_s,
-                                               grad_ys=dy3[..., P:])
-            if dyt is not None:   # the gate part of dY^T (H rows) from the transpose kernel
+            _, dh, dbias = gate_heads_backward(y3[..., P:P + S], b32, hagg, dsh.view(B, N, P), heads, rope_s,
+                                               grad_ys=dy3[..., P:P + S])
+            if dyt is not None:   # the gate part of dY^T (with the padding rows) from the transpose kernel
                 _transpose_into(dy[:, P:], dyt[P:], "transpose_dy")
         else:
-            dh, dbias = gate_backward(y3[..., P:], b32, hagg, dsh.view(B, N, P), dy3[..., P:], rope_s,
-                                      grad_ys_t=None if dyt is None else dyt[P:], grad_ys_rows=dy[:, P:])
+            dh, dbias = gate_backward(y3[..., P:P + S], b32, hagg, dsh.view(B, N, P), dy3[..., P:P + S], rope_s,
+                                      grad_ys_t=None if dyt is None else dyt[P:P + S],
+                                      grad_ys_rows=dy[:, P:P + S])
         if grad_hagg is not None:
             dh = dh + grad_hagg.float()
         dcoeff = agg_backward(y3[..., :P], c32, k, frame_len, dh, dy3[..., :P], mask, count, n_past, rope_h,
@@ -754,6 +783,8 @@ class _PoMLayer(torch.autograd.Function):
             w = n_past / (n_past + torch.arange(nf, device=dev, dtype=torch.float32) + 1.0)
             g_carry = (dh * w.view(1, nf, 1)).sum(dim=1, keepdim=True).to(dt)
         tq, tb, tc, ta, tab = ctx.dtypes
+        if dw_qc is not None and dw_qc.shape[0] != P + S:
+            dw_qc = dw_qc[:P + S]   # the padding rows' gradient is not a parameter's
         return (None if dx is None else dx.view(B, N, D), None if dw_qc is None else dw_qc.to(tq),
                 dbias.to(tb), dcoeff.to(tc), None if dw_ag is None else dw_ag.to(ta),
                 None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None, None, None)
