@@ -284,8 +284,8 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_chunk(const AggParams p) {
     for (int u = 0; u < U; ++u) {
       const int64_t rr = W.row(base, u, clamp);
       const T* row = xb + rr * p.sxn;
-      bf.v1[u].load(row + map.c1);
-      if constexpr (ROPE) bf.v2[u].load(row + map.c2);
+      bf.v1[u].load_stream(row + map.c1);
+      if constexpr (ROPE) bf.v2[u].load_stream(row + map.c2);
       if constexpr (MASKED) bf.wv[u] = p.mask[b * p.msb + rr * p.msn];
     }
   };
@@ -534,8 +534,8 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
     for (int u = 0; u < U; ++u) {
       const int64_t rr = W.row(base, u, clamp);
       const T* row = xb + rr * p.sxn;
-      bf.v1[u].load(row + map.c1);
-      if constexpr (ROPE) bf.v2[u].load(row + map.c2);
+      bf.v1[u].load_stream(row + map.c1);
+      if constexpr (ROPE) bf.v2[u].load_stream(row + map.c2);
       if constexpr (MASKED) bf.mv[u] = p.mask[b * p.msb + rr * p.msn];
     }
   };

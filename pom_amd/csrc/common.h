@@ -204,6 +204,36 @@ __device__ __forceinline__ float hsig_grad(float z) {
 // Raw vector of V elements of T held in registers as loaded (16-byte or
 // narrower memory operations), widened to fp32 one element at a time.
 // ---------------------------------------------------------------------------
+// Loads of data read once per launch (token rows) carry the non-temporal
+// hint: the line is not kept in the caches at the expense of others, so a
+// stream does not evict (and force the write-back of) the dirty lines the
+// previous kernel left behind.  Set POM_STREAM_NT=0 to compile plain loads.
+#ifndef POM_STREAM_NT
+#define POM_STREAM_NT 1
+#endif
+template <typename R>
+__device__ __forceinline__ R load_stream_raw(const R* __restrict__ p) {
+#if POM_STREAM_NT
+  if constexpr (sizeof(R) == 16) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    R r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+  } else if constexpr (sizeof(R) == 8) {
+    typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+    const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+    R r;
+    __builtin_memcpy(&r, &v, 8);
+    return r;
+  } else {
+    return __builtin_nontemporal_load(p);
+  }
+#else
+  return *p;
+#endif
+}
+
 template <typename T, int V>
 struct Pack {
   using IO = VecIO<T, V>;
@@ -212,6 +242,12 @@ struct Pack {
   __device__ __forceinline__ void load(const T* __restrict__ p) {
 #pragma unroll
     for (int op = 0; op < IO::kOps; ++op) r[op] = *reinterpret_cast<const typename IO::Raw*>(p + op * IO::kPer);
+  }
+  // the same for data read once (see load_stream_raw)
+  __device__ __forceinline__ void load_stream(const T* __restrict__ p) {
+#pragma unroll
+    for (int op = 0; op < IO::kOps; ++op)
+      r[op] = load_stream_raw(reinterpret_cast<const typename IO::Raw*>(p + op * IO::kPer));
   }
   __device__ __forceinline__ float get(int i) const {
     return to_f32<T>(reinterpret_cast<const T*>(r)[i]);

@@ -72,8 +72,8 @@ __global__ void __launch_bounds__(kThreads) gate_fwd_kernel(const GateParams p, 
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const T* row = yb + W.row(base, u, clamp) * p.ysn;
-      bf.y1[u].load(row + map.c1);
-      if constexpr (ROPE) bf.y2[u].load(row + map.c2);
+      bf.y1[u].load_stream(row + map.c1);
+      if constexpr (ROPE) bf.y2[u].load_stream(row + map.c2);
     }
   };
   auto step = [&](const Buf& bf, int64_t base, auto tail_tag) {
@@ -192,11 +192,11 @@ __global__ void __launch_bounds__(kThreads) gate_bwd_kernel(const GateParams p, 
       const int64_t rr = W.row(base, u, clamp);
       const T* yrow = yb + rr * p.ysn;
       const T* grow = gb + rr * p.dsn;
-      bf.y1[u].load(yrow + map.c1);
-      bf.g1[u].load(grow + map.c1);
+      bf.y1[u].load_stream(yrow + map.c1);
+      bf.g1[u].load_stream(grow + map.c1);
       if constexpr (ROPE) {
-        bf.y2[u].load(yrow + map.c2);
-        bf.g2[u].load(grow + map.c2);
+        bf.y2[u].load_stream(yrow + map.c2);
+        bf.g2[u].load_stream(grow + map.c2);
       }
     }
   };

@@ -81,8 +81,8 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanParams p) 
     for (int u = 0; u < U; ++u) {
       if (r + u < rend) {
         const T* row = xb + (r + u) * p.sxn;
-        v1[u].load(row + map.c1);
-        if constexpr (ROPE) v2[u].load(row + map.c2);
+        v1[u].load_stream(row + map.c1);
+        if constexpr (ROPE) v2[u].load_stream(row + map.c2);
       }
     }
 #pragma unroll
@@ -182,10 +182,10 @@ __global__ void __launch_bounds__(kThreads) scan_bwd_kernel(const ScanParams p) 
       const int64_t n = r - u;
       if (n >= rbeg) {
         const T* row = xb + n * p.sxn;
-        v1[u].load(row + map.c1);
+        v1[u].load_stream(row + map.c1);
         load_f32<CPT>(gob + n * p.P + map.c1, g1[u]);
         if constexpr (ROPE) {
-          v2[u].load(row + map.c2);
+          v2[u].load_stream(row + map.c2);
           load_f32<CPT>(gob + n * p.P + map.c2, g2[u]);
         }
       }
