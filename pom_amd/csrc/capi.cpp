@@ -52,17 +52,22 @@ struct Tune {
   int64_t agg_target_wg = 512;   // aggregation: one chunk per row when B * slabs reaches it
   int64_t min_rows = 128;
   int64_t scan_target_wg = 2048;
+  int heads_rows = 1;              // per-head backward: row walk where it applies
+  int64_t heads_rows_target = 512; // per-head row walk: workgroups wanted
   Tune() {
     if (const char* s = getenv("POM_AMD_LPR_LOG2")) lpr_log2 = atoi(s);
     if (const char* s = getenv("POM_AMD_TARGET_WG")) target_wg = atoll(s);
     if (const char* s = getenv("POM_AMD_AGG_TARGET_WG")) agg_target_wg = atoll(s);
     if (const char* s = getenv("POM_AMD_MIN_ROWS")) min_rows = atoll(s);
     if (const char* s = getenv("POM_AMD_SCAN_TARGET_WG")) scan_target_wg = atoll(s);
+    if (const char* s = getenv("POM_AMD_HEADS_ROWS")) heads_rows = atoi(s);
+    if (const char* s = getenv("POM_AMD_HEADS_ROWS_TARGET")) heads_rows_target = atoll(s);
     if (lpr_log2 < 0 || lpr_log2 > 6) lpr_log2 = 3;
     if (target_wg < 1) target_wg = 1024;
     if (agg_target_wg < 1) agg_target_wg = 512;
     if (min_rows < 1) min_rows = 128;
     if (scan_target_wg < 1) scan_target_wg = 2048;
+    if (heads_rows_target < 1) heads_rows_target = 512;
   }
 };
 const Tune& tune() {
@@ -382,6 +387,25 @@ int heads_tpw(int64_t N, int64_t L) {
   return (L == 1 || L % (4 * kHeadTile) == 0) ? 4 : 1;
 }
 
+// Row-walk backward: tokens per walk, the largest of 256 .. 8 that gives the
+// target workgroup count (walks stay inside one hagg group); 0 when the row
+// walk does not apply (single-token groups, head_dim not a multiple of 8, a
+// row wider than one workgroup, or more heads than its reduction slots).
+int64_t heads_rows_wt(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups) {
+  if (!tune().heads_rows || groups <= 0 || N % groups) return 0;
+  const int64_t L = N / groups;
+  if (L == 1 || P % 8 || P % H || (P / H) % 8) return 0;
+  if (pom::heads_rows_threads(P, H) > 1024 || pom::heads_rows_smem(P, H) > 64 * 1024) return 0;
+  if (B > 65535) return 0;
+  int64_t pick = 0;
+  for (int64_t wt : {256, 128, 64, 32, 16, 8}) {
+    if (groups > 1 && L % wt) continue;
+    pick = wt;
+    if (B * cdiv(N, wt) >= tune().heads_rows_target) break;
+  }
+  return pick;
+}
+
 size_t heads_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups) {
   int64_t nch = 1, tok_wgs = 1;
   for (int V : {1, 2, 4, 8}) {   // every chunk width the call may choose
@@ -392,7 +416,13 @@ size_t heads_ws_bytes(int64_t B, int64_t N, int64_t P, int64_t H, int64_t groups
   const size_t general = carve_bytes({B * N * H, tok_wgs * H, B * nch * P});
   const int64_t nct = cdiv(P, kHeadTile), ntt = cdiv(N, kHeadTile);
   const size_t tile = carve_bytes({B * N * nct * heads_nhm(P, H), B * ntt * P, B * N * H});
-  return general > tile ? general : tile;
+  size_t best = general > tile ? general : tile;
+  if (const int64_t wt = heads_rows_wt(B, N, P, H, groups)) {
+    const int64_t nw = cdiv(N, wt);
+    const size_t rows = carve_bytes({B * nw * P, B * nw * H});
+    if (rows > best) best = rows;
+  }
+  return best;
 }
 
 int setup_heads(pom::HeadsParams& p, int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int64_t H,
@@ -689,8 +719,19 @@ int pom_gate_heads_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t
   p.dbias = {grad_bias, param_dtype};
   if (p.tile && !aligned(grad_hagg, 16)) p.tile = 0;   // per-token rows are stored 8 floats at a time
   if (int r = need_ws(workspace, workspace_bytes, heads_ws_bytes(B, N, P, H, groups))) return r;
+  // row walk: 16-byte chunks of dsh and hagg (the tile path's operand conditions)
+  const int64_t wt = heads_rows_wt(B, N, P, H, groups);
+  if (wt > 0 && aligned(hagg, 16) && aligned(grad_sh->data, 16) && grad_sh->stride_b % 8 == 0 &&
+      grad_sh->stride_n % 8 == 0) {
+    p.rows = 1;
+    p.wt = wt;
+    p.ntt = cdiv(N, wt);
+  }
   Carve c{static_cast<char*>(workspace), 0};
-  if (p.tile) {
+  if (p.rows) {
+    p.part_h = c.take<float>(B * p.ntt * P);
+    p.dzbuf = c.take<float>(B * p.ntt * H);
+  } else if (p.tile) {
     p.dpart = c.take<float>(B * N * cdiv(P, kHeadTile) * p.nhm);
     p.part_h = c.take<float>(B * p.ntt * P);
     p.dzbuf = c.take<float>(B * N * H);

@@ -460,7 +460,8 @@ static __global__ void __launch_bounds__(kThreads) heads_tile_finalize(const Hea
   const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (p.L > 1 && idx < p.B * p.G * p.P) {
     const int64_t c = idx % p.P, bg = idx / p.P, b = bg / p.G, g = bg - b * p.G;
-    const int64_t per = p.L / (kTT * p.tpw);   // walks per group
+    // walks per group (a single group may end in a partial walk)
+    const int64_t per = p.G == 1 ? p.ntt : p.L / (p.rows ? p.wt : kTT * p.tpw);
     const float* src = p.part_h + (b * p.ntt + g * per) * p.P + c;
     float s = 0.0f;
     int64_t k = 0;
@@ -475,7 +476,8 @@ static __global__ void __launch_bounds__(kThreads) heads_tile_finalize(const Hea
     p.dhagg[idx] = s;
   }
   if (p.dbias.ptr && blockIdx.x < p.H) {
-    const int64_t h = blockIdx.x, rows = (p.B * p.N + kDzT - 1) / kDzT;   // dz-kernel partials
+    // dz partial rows: one per walk (row path) or per 16 tokens (dz kernel)
+    const int64_t h = blockIdx.x, rows = p.rows ? p.B * p.ntt : (p.B * p.N + kDzT - 1) / kDzT;
     float s = 0.0f;
     for (int64_t r = threadIdx.x; r < rows; r += kThreads) s += p.dzbuf[r * p.H + h];
     red[threadIdx.x] = s;
@@ -485,6 +487,157 @@ static __global__ void __launch_bounds__(kThreads) heads_tile_finalize(const Hea
       __syncthreads();
     }
     if (threadIdx.x == 0) param_set(p.dbias, h, red[0]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row path of the backward (head_dim % 8 == 0, groups of more than one token).
+// A workgroup walks p.wt tokens of one batch row over all P channels: thread j
+// owns channels 8j..8j+7, which lie in one head.  Per step of kRowU tokens
+// each thread adds s' * dsh into its dhagg partial (registers, whole walk) and
+// writes its chunk's share of the head dot product into LDS; after one
+// barrier, thread (t, h) sums head h's chunks for token t, applies R^T and
+// hardsigmoid', writes dY_s and keeps its dz sum.  The dot products are
+// double-buffered, so a step needs no second barrier.  dsh is read once and
+// no partial leaves the workgroup except the walk's dhagg and dz sums.
+// ---------------------------------------------------------------------------
+constexpr int kRowU = kHeadsRowU;
+
+template <typename T, int MODE>
+__global__ void __launch_bounds__(1024) heads_bwd_rows(const HeadsParams p) {
+  extern __shared__ float dots[];   // [2][kRowU][J]; reused for the dz sums at the end
+  const int tid = threadIdx.x;
+  const int J = (int)(p.P / 8), hd8 = (int)(p.hd / 8), H = (int)p.H;
+  const int64_t b = blockIdx.y, w = blockIdx.x;
+  const int64_t nbeg = w * p.wt, nend = nbeg + p.wt < p.N ? nbeg + p.wt : p.N;
+  const int64_t grp = nbeg / p.L;
+  const T* yb = reinterpret_cast<const T*>(p.ys) + b * p.ysb;
+
+  // chunk role: channels c0..c0+7 of head hj
+  const bool own = tid < J;
+  const int j = own ? tid : 0;
+  const int64_t c0 = (int64_t)j * 8, hj = j / hd8;
+  int blk = 0, table = 0;
+  int64_t col = 0, partner = hj;
+  if constexpr (MODE != MODE_PLAIN) head_pair<MODE>(p.H, hj, blk, col, partner, table);
+  float bj[2] = {0.0f, 0.0f};
+  if (p.bias.ptr) param_gather<2>(p.bias, [&](int q) { return q ? partner : hj; }, bj);
+  float hv[8];
+  {
+    Pack<T, 8> hp;
+    hp.load(reinterpret_cast<const T*>(p.hagg) + (b * p.G + grp) * p.P + c0);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) hv[v] = hp.get(v);
+  }
+  const T* gb = reinterpret_cast<const T*>(p.dsh) + b * p.dsb + c0;
+
+  // reduction role: slot (rt, hr) for tid < kRowU * H
+  const bool red = tid < kRowU * H;
+  const int rt = red ? tid / H : 0, hr = red ? tid - rt * H : 0;
+  int rblk = 0, rtable = 0;
+  int64_t rcol = 0, rpartner = hr;
+  if constexpr (MODE != MODE_PLAIN) head_pair<MODE>(p.H, hr, rblk, rcol, rpartner, rtable);
+  const float bz = (red && p.bias.ptr) ? param_get(p.bias, hr) : 0.0f;
+  float dzacc = 0.0f;
+
+  float acc[8];
+#pragma unroll
+  for (int v = 0; v < 8; ++v) acc[v] = 0.0f;
+  Pack<T, 8> gp[kRowU];
+  T y0[kRowU], y1[kRowU], yz = T();
+  // one step's loads (the chunk rows and gate inputs, and the reduction slot's
+  // y_s), all issued together: a load issued after them would wait for them
+  // all; rows past the walk re-read its last row (never used)
+  auto load = [&](int64_t n0) {
+    if (own) {
+#pragma unroll
+      for (int u = 0; u < kRowU; ++u) {
+        const int64_t n = n0 + u < nend ? n0 + u : nend - 1;
+        gp[u].load(gb + n * p.dsn);
+        y0[u] = yb[n * p.ysn + hj];
+        if constexpr (MODE != MODE_PLAIN) y1[u] = yb[n * p.ysn + partner];
+      }
+    }
+    if (red) yz = yb[(n0 + rt < nend ? n0 + rt : nend - 1) * p.ysn + hr];
+  };
+  load(nbeg);
+  int buf = 0;
+  for (int64_t n0 = nbeg; n0 < nend; n0 += kRowU, buf ^= 1) {
+    float* d = dots + buf * kRowU * J;
+    const float zy = to_f32<T>(yz);   // this step's reduction-slot y_s
+    if (own) {
+#pragma unroll
+      for (int u = 0; u < kRowU; ++u) {
+        const int64_t n = n0 + u;
+        float s = hsig(to_f32<T>(y0[u]) + bj[0]);
+        if constexpr (MODE != MODE_PLAIN) {
+          float cs, sn;
+          table_cs(p.rope, table, n < nend ? n : nend - 1, col, cs, sn);
+          const float sp = hsig(to_f32<T>(y1[u]) + bj[1]);
+          s = blk ? s * cs + sp * sn : s * cs - sp * sn;
+        }
+        const bool in = n < nend;
+        float dot = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const float g = gp[u].get(v);
+          dot = fmaf(g, hv[v], dot);
+          acc[v] = fmaf(g, in ? s : 0.0f, acc[v]);
+        }
+        d[u * J + j] = in ? dot : 0.0f;
+      }
+    }
+    if (n0 + kRowU < nend) load(n0 + kRowU);   // in flight during the reduction below
+    __syncthreads();   // the step's dot products are in LDS
+    if (red && n0 + rt < nend) {
+      const int64_t n = n0 + rt;
+      const float* dr = d + rt * J;
+      float ds = 0.0f;
+      for (int k = 0; k < hd8; ++k) ds += dr[hr * hd8 + k];
+      if constexpr (MODE != MODE_PLAIN) {
+        float dq = 0.0f;
+        for (int k = 0; k < hd8; ++k) dq += dr[rpartner * hd8 + k];
+        float cs, sn;
+        table_cs(p.rope, rtable, n, rcol, cs, sn);
+        ds = rblk ? ds * cs - dq * sn : ds * cs + dq * sn;
+      }
+      const float z = zy + bz;
+      const float dz = ds * hsig_grad(z);
+      reinterpret_cast<T*>(p.dys)[b * p.dyb + n * p.dyn + hr] = from_f32<T>(dz);
+      dzacc += dz;
+    }
+  }
+  const int64_t walk = b * p.ntt + w;
+  if (own) store_f32<8>(p.part_h + walk * p.P + c0, acc);
+  __syncthreads();   // every step's readers of the dot products are done
+  if (red) dots[tid] = dzacc;   // [rt][hr]
+  __syncthreads();
+  if (tid < H) {
+    float sum = 0.0f;
+    for (int t = 0; t < kRowU; ++t) sum += dots[t * H + tid];
+    p.dzbuf[walk * H + tid] = sum;
+  }
+}
+
+template <typename T, int MODE>
+hipError_t heads_rows_bwd_m(const HeadsParams& p, hipStream_t st) {
+  const dim3 grid((unsigned)p.ntt, (unsigned)p.B);
+  hipLaunchKernelGGL((heads_bwd_rows<T, MODE>), grid, dim3(heads_rows_threads(p.P, p.H)),
+                     heads_rows_smem(p.P, p.H), st, p);
+  if (hipError_t e = hipGetLastError(); e != hipSuccess) return e;
+  const int64_t flat = (p.B * p.G * p.P + kThreads - 1) / kThreads;
+  const int64_t fb = flat > p.H ? flat : (p.dbias.ptr ? p.H : flat);
+  hipLaunchKernelGGL(heads_tile_finalize, dim3((unsigned)fb), dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t heads_rows_bwd(const HeadsParams& p, hipStream_t st) {
+  switch (p.mode) {
+    case MODE_PLAIN: return heads_rows_bwd_m<T, MODE_PLAIN>(p, st);
+    case MODE_ROPE1D: return heads_rows_bwd_m<T, MODE_ROPE1D>(p, st);
+    case MODE_ROPE2D: return heads_rows_bwd_m<T, MODE_ROPE2D>(p, st);
+    default: return hipErrorInvalidValue;
   }
 }
 
@@ -593,6 +746,7 @@ hipError_t heads_fwd_t(const HeadsParams& p, hipStream_t st) {
 
 template <typename T>
 hipError_t heads_bwd_t(const HeadsParams& p, hipStream_t st) {
+  if (p.rows) return heads_rows_bwd<T>(p, st);
   if (p.tile) return heads_tile_bwd<T>(p, st);
   POM_V_SWITCH(T, p.V, heads_bwd_v, p, st)
 }

@@ -248,11 +248,30 @@ struct HeadsParams {
   int64_t nhm = 1;                // heads a channel tile can touch (dot-partial stride)
   float* dpart = nullptr;         // (B * N, channel tiles, nhm) per-head dot partials
   float* dzbuf = nullptr;         // (cdiv(B * N, 16), H) fp32 dz sums per 16-token group
+                                  // | row path: (B * ntt, H) per walk
+
+  // row path (backward): a workgroup walks wt tokens of one batch row over all
+  // P channels; ntt = cdiv(N, wt) walks per row, part_h (B, ntt, P)
+  int rows = 0;
+  int64_t wt = 0;
 };
 
 // LDS of the token-row backward kernel: per wave, cpr chunk dots and two
 // H-vectors.
 inline size_t heads_token_smem_bytes(int64_t cpr, int64_t H) { return sizeof(float) * 4 * (size_t)(cpr + 2 * H); }
+
+// Row-walk backward of per-head gating: tokens per step, threads per
+// workgroup (one per 8-channel chunk and at least one per (step token, head)
+// slot, whole 64-lane waves) and LDS bytes (double-buffered dot products).
+constexpr int kHeadsRowU = 8;
+inline int heads_rows_threads(int64_t P, int64_t H) {
+  const int64_t need = P / 8 > kHeadsRowU * H ? P / 8 : kHeadsRowU * H;
+  return (int)((need + 63) / 64 * 64);
+}
+inline size_t heads_rows_smem(int64_t P, int64_t H) {
+  const int64_t a = 2 * kHeadsRowU * (P / 8), c = kHeadsRowU * H;
+  return sizeof(float) * (size_t)(a > c ? a : c);
+}
 
 template <typename T> hipError_t heads_fwd_t(const HeadsParams& p, hipStream_t st);
 template <typename T> hipError_t heads_bwd_t(const HeadsParams& p, hipStream_t st);

@@ -63,9 +63,10 @@ def _case(device, B, N, P, H, G, dtype, rope=None, bias=True, strided=True, seed
                                        (2, 30, 60, 6, 5), (2, 256, 128, 8, 2), (2, 100, 40, 5, 1),
                                        (1, 64, 200, 25, 64)])
 def test_heads_plain(device, B, N, P, H, G, dtype):
-    # tile path: 64-token groups or single-token groups with P % 8 == 0 (head_dim 16, 36, 12, 16,
-    # 8 — 64-channel tiles touching up to 9 heads); general path: 32-token frames, 33 tokens,
-    # head_dim 9 (scalar chunks) and 10 (pairs), P = 40 in a 100-token row
+    # backward paths: row walk where head_dim % 8 == 0 and groups hold many tokens (head_dim 16
+    # with one or two groups, 8 with 33 and 100 tokens: partial last walks); tile path for
+    # head_dim 36, 12 and single-token groups (64-channel tiles touching up to 9 heads); general
+    # path for 32-token frames of head_dim 12, head_dim 9 (scalar chunks) and 10 (pairs)
     _case(device, B, N, P, H, G, dtype)
 
 
@@ -89,10 +90,7 @@ def test_heads_no_bias_contiguous(device):
     _case(device, 2, 64, 128, 8, 1, torch.float32, bias=False, strided=False)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("G", [1, 4])
-def test_heads_rope1d(device, dtype, G):
-    N, P, H = 128, 96, 8
+def _rope1d_case(device, N, P, H, G, dtype):
     hd = P // H
     fc, fs = O.precompute_freqs_1d(P, 256)
     tc, ts = fc[:, ::hd // 2][:, :H // 2], fs[:, ::hd // 2][:, :H // 2]   # pom/pom_rope.py:417-437
@@ -101,6 +99,20 @@ def test_heads_rope1d(device, dtype, G):
             "spec": lambda dev: _lib.RopeSpec(_lib.ROPE_1D, [tc.contiguous().to(dev), ts.contiguous().to(dev)],
                                               pos.to(dev))}
     _case(device, 2, N, P, H, G, dtype, rope=rope)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("G", [1, 4])
+def test_heads_rope1d(device, dtype, G):
+    # head_dim 12: the tile backward
+    _rope1d_case(device, 128, 96, 8, G, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("G", [1, 4])
+def test_heads_rope1d_row_walk(device, dtype, G):
+    # head_dim 16 and groups of 32 or 128 tokens: the row-walk backward
+    _rope1d_case(device, 128, 128, 8, G, dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -120,6 +132,13 @@ def test_heads_c2_width(device):
     """The reference benches' configuration: n_sel_heads = 16 at D = 1152,
     expand 2 (P = 2304, head_dim 144), bf16."""
     _case(device, 2, 512, 2304, 16, 1, torch.bfloat16)
+
+
+@pytest.mark.parametrize("B,N,P,H,G", [(64, 1024, 64, 4, 4), (16, 1024, 256, 4, 1)])
+def test_heads_row_walk_lengths(device, B, N, P, H, G):
+    """Row-walk backward at batch sizes that pick 128-token walks (two per
+    256-token group) and 32-token walks (the c2h batch, one group)."""
+    _case(device, B, N, P, H, G, torch.bfloat16)
 
 
 def test_heads_modules_use_the_kernels(device):
