@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 import pom_amd  # noqa: E402
 
 
-@pytest.mark.parametrize("variant", ["mean", "block", "masked", "rope2d"])
+@pytest.mark.parametrize("variant", ["mean", "block", "masked", "rope2d", "heads"])
 def test_layer_graph_replays_match_eager(device, variant):
     torch.manual_seed(0)
     B, N, D = 4, 256, 128
@@ -21,6 +21,10 @@ def test_layer_graph_replays_match_eager(device, variant):
         pos = torch.stack(torch.meshgrid(torch.arange(16), torch.arange(16), indexing="ij"), -1).reshape(-1, 2)
         pos = pos.to(device)
         fwd = lambda x: m(x, positions_hw=pos)
+    elif variant == "heads":
+        # per-head gating: Y is P + 4 = 260 columns, padded to 320 (zero rows appended to W_qc)
+        m = pom_amd.PoM(D, 2, 2, n_sel_heads=4).to(device, torch.bfloat16)
+        fwd = lambda x: m(x)
     else:
         m = pom_amd.PoM(D, 2, 2).to(device, torch.bfloat16)
         if variant == "block":
