@@ -366,8 +366,9 @@ KERNEL_NAMES = {
     "gate_fwd": ["gate_fwd_kernel"],
     "gate_bwd": ["gate_bwd_kernel", "gate_bwd_finalize"],
     "transpose": ["transpose_blocks", "transpose_elems"],   # x^T, g^T and the weights, per step
-    "gate_heads_fwd": ["heads_fwd_kernel"],
-    "gate_heads_bwd": ["heads_bwd_token_kernel", "heads_bwd_hagg_kernel", "heads_bwd_finalize"],
+    "gate_heads_fwd": ["heads_fwd_kernel", "heads_fwd_tile"],
+    "gate_heads_bwd": ["heads_bwd_token_kernel", "heads_bwd_hagg_kernel", "heads_bwd_finalize", "heads_bwd_tile",
+                       "heads_bwd_dz", "heads_tile_finalize", "heads_bwd_rows"],
 }
 
 
@@ -389,7 +390,7 @@ COPY_CALIB_MIB = 144   # pmc_summary expects the calibration run made with --cop
 
 def _is_gate_bwd(name: str) -> bool:
     """The gate backward's main kernel (full-width or per-head)."""
-    return any(k in name for k in ("gate_bwd_kernel", "heads_bwd_tile", "heads_bwd_token_kernel"))
+    return any(k in name for k in ("gate_bwd_kernel", "heads_bwd_rows", "heads_bwd_tile", "heads_bwd_token_kernel"))
 
 
 def _gemm_dispatches(db: str):
