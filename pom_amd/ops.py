@@ -175,6 +175,21 @@ def _padded_width(p: int, s: int) -> int:
     return (p + s + 63) // 64 * 64
 
 
+_zero_cache: dict = {}
+
+
+def _zero_rows(n: int, cols: int, dt: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A cached all-zero (n, cols) block; it is only ever read.  Under stream
+    capture a fresh block (the graph's own memory, filled on every replay)."""
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(n, cols, dtype=dt, device=device)
+    key = (n, cols, dt, device)
+    z = _zero_cache.get(key)
+    if z is None:
+        z = _zero_cache[key] = torch.zeros(n, cols, dtype=dt, device=device)
+    return z
+
+
 def _qc_weight(w: torch.Tensor, dt: torch.dtype, rows: int) -> torch.Tensor:
     """W_qc in dtype dt with zero rows appended up to ``rows`` (the padded
     projection width), cached per weight version."""
@@ -182,9 +197,7 @@ def _qc_weight(w: torch.Tensor, dt: torch.dtype, rows: int) -> torch.Tensor:
         u = u.detach().to(dt)
         if u.shape[0] == rows:
             return u
-        out = torch.zeros(rows, u.shape[1], dtype=dt, device=u.device)
-        out[:u.shape[0]] = u
-        return out
+        return torch.cat([u, _zero_rows(rows - u.shape[0], u.shape[1], dt, u.device)])   # one kernel
     if w.dtype == dt and w.shape[0] == rows:
         return w
     return _derived(_pad_cache, w, make)
