@@ -48,7 +48,8 @@ int ilog2_ceil(int64_t v) {
 // shortest chunk worth its own workgroup.
 struct Tune {
   int lpr_log2 = 3;        // 8 lanes x 16 bytes = 128-byte row segments
-  int64_t target_wg = 1024;      // gating kernels
+  int64_t target_wg = 1024;      // per-head general path, polynomial features
+  int64_t gate_target_wg = 2048; // full-width gating kernels (all frames; RoPE lanes count twice)
   int64_t agg_target_wg = 512;   // aggregation: one chunk per row when B * slabs reaches it
   int64_t min_rows = 128;
   int64_t scan_target_wg = 2048;
@@ -57,6 +58,7 @@ struct Tune {
   Tune() {
     if (const char* s = getenv("POM_AMD_LPR_LOG2")) lpr_log2 = atoi(s);
     if (const char* s = getenv("POM_AMD_TARGET_WG")) target_wg = atoll(s);
+    if (const char* s = getenv("POM_AMD_GATE_TARGET_WG")) gate_target_wg = atoll(s);
     if (const char* s = getenv("POM_AMD_AGG_TARGET_WG")) agg_target_wg = atoll(s);
     if (const char* s = getenv("POM_AMD_MIN_ROWS")) min_rows = atoll(s);
     if (const char* s = getenv("POM_AMD_SCAN_TARGET_WG")) scan_target_wg = atoll(s);
@@ -64,6 +66,7 @@ struct Tune {
     if (const char* s = getenv("POM_AMD_HEADS_ROWS_TARGET")) heads_rows_target = atoll(s);
     if (lpr_log2 < 0 || lpr_log2 > 6) lpr_log2 = 3;
     if (target_wg < 1) target_wg = 1024;
+    if (gate_target_wg < 1) gate_target_wg = 2048;
     if (agg_target_wg < 1) agg_target_wg = 512;
     if (min_rows < 1) min_rows = 128;
     if (scan_target_wg < 1) scan_target_wg = 2048;
@@ -112,6 +115,20 @@ void choose_slabs(pom::Geom& g) {
 void choose_chunks(pom::Geom& g, int64_t B, int64_t target) {
   int64_t cpf = 1;
   while (B * cpf * g.nslabs < target && cdiv(g.L, 2 * cpf) >= tune().min_rows) cpf *= 2;
+  g.RC = cdiv(g.L, cpf);
+  g.cpf = cdiv(g.L, g.RC);
+  g.nch = g.F * g.cpf;
+}
+
+// Gating-kernel chunks.  The gate forward is elementwise and only the
+// backward's dhagg / dbias sums follow the chunking, so unlike the
+// aggregation's, the count may depend on the frames: the workgroups of all
+// frames together are held near the target.  A RoPE lane carries both
+// halves of its pairs, so RoPE modes aim at half as many workgroups.
+void choose_gate_chunks(pom::Geom& g, int64_t B, bool rope) {
+  const int64_t target = rope ? tune().gate_target_wg / 2 : tune().gate_target_wg;
+  int64_t cpf = 1;
+  while (B * g.F * cpf * g.nslabs < target && cdiv(g.L, 2 * cpf) >= tune().min_rows) cpf *= 2;
   g.RC = cdiv(g.L, cpf);
   g.cpf = cdiv(g.L, g.RC);
   g.nch = g.F * g.cpf;
@@ -337,7 +354,7 @@ int setup_gate(pom::GateParams& p, int& per_token, int dtype, int64_t B, int64_t
     p.g.F = groups;
     p.g.L = N / groups;
   }
-  choose_chunks(p.g, B, tune().target_wg);
+  choose_gate_chunks(p.g, B, is_rope(p.mode));
   if (p.g.nch > 65535 || B > 65535) return fail(POM_ERR_UNSUPPORTED, "grid too large");
   return POM_OK;
 }
