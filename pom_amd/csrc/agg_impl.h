@@ -438,7 +438,9 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
   constexpr int CPT2 = Map::CPT2;
   constexpr bool ROPE = Mode_<MODE>::rope;
   constexpr bool MASKED = mode_masked(MODE);
-  constexpr int U = TR && !ROPE ? 4 : Mode_<MODE>::U;
+  // with the channel-major copy: 4 rows in flight, 2 for RoPE (its pairs and
+  // tile slots double the per-lane state; 4 fills all 256 VGPRs)
+  constexpr int U = TR ? (ROPE ? 2 : 4) : Mode_<MODE>::U;
   __shared__ float red[kWaves][kMaxLpr * CPT2];
 
   const LaneGeom G(p.g.lpr_log2);
@@ -528,6 +530,7 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
   struct Buf {
     Pack<T, CPT> v1[U], v2[ROPE ? U : 1];
     float mv[U];
+    int tp[ROPE ? U : 1];   // table positions, loaded with the rows
   };
   auto load = [&](Buf& bf, int64_t base, bool clamp) {
 #pragma unroll
@@ -535,7 +538,10 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
       const int64_t rr = W.row(base, u, clamp);
       const T* row = xb + rr * p.sxn;
       bf.v1[u].load_stream(row + map.c1);
-      if constexpr (ROPE) bf.v2[u].load_stream(row + map.c2);
+      if constexpr (ROPE) {
+        bf.v2[u].load_stream(row + map.c2);
+        bf.tp[u] = rope_pos(p.rope, map.table, rr);
+      }
       if constexpr (MASKED) bf.mv[u] = p.mask[b * p.msb + rr * p.msn];
     }
   };
@@ -553,7 +559,7 @@ __device__ __forceinline__ void agg_bwd_body(const AggParams& p) {
       float gv1[CPT], gv2[CPT];
       if constexpr (ROPE) {
         float cs[CPT], sn[CPT];
-        load_table<CPT>(p.rope, map.table, n, map.tcol, cs, sn);
+        load_table_at<CPT>(p.rope, map.table, bf.tp[u], map.tcol, cs, sn);
         bool keep = in;
         float mw = 1.0f;
         if constexpr (MASKED) {

@@ -84,6 +84,23 @@ __device__ __forceinline__ int64_t slot_chan(int64_t s, int64_t P) {
 // cos/sin of token n for CPT consecutive rotation pairs starting at table column
 // tcol.  Positions outside the table are clamped so a bad position can never
 // read outside the table.
+// The two halves of the lookup: the position (a load that the streaming
+// kernels issue together with the step's row loads) and the table entries
+// at that position.
+__device__ __forceinline__ int rope_pos(const RopeTables& t, int table, int64_t n) {
+  const int64_t v = t.pos[n * t.pos_sn + table];
+  return v < 0 ? -1 : (v > 0x7fffffff ? 0x7fffffff : (int)v);   // saturated: the table clamp sees the same side
+}
+
+template <int CPT>
+__device__ __forceinline__ void load_table_at(const RopeTables& t, int table, int pos, int64_t tcol,
+                                              float (&cs)[CPT], float (&sn)[CPT]) {
+  const int64_t rows = table ? t.rows1 : t.rows0;
+  const int64_t r = pos < 0 ? 0 : (pos >= rows ? rows - 1 : pos);
+  load_f32<CPT>((table ? t.cos1 : t.cos0) + r * t.stride + tcol, cs);
+  load_f32<CPT>((table ? t.sin1 : t.sin0) + r * t.stride + tcol, sn);
+}
+
 template <int CPT>
 __device__ __forceinline__ void load_table(const RopeTables& t, int table, int64_t n, int64_t tcol,
                                            float (&cs)[CPT], float (&sn)[CPT]) {
