@@ -141,6 +141,16 @@ def test_heads_row_walk_lengths(device, B, N, P, H, G):
     _case(device, B, N, P, H, G, torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,N,P,H,G", [(1, 40, 8192, 8, 1), (1, 24, 8256, 8, 1), (2, 60, 64, 4, 5)])
+def test_heads_row_walk_limits(device, B, N, P, H, G, dtype):
+    """The row walk at its widest row (P = 8192: 1024 threads, 64 KB of LDS), a
+    row of 1032 chunks (over one workgroup: the general backward), and head_dim
+    16 with 12-token groups (no walk length divides the group: the general
+    backward)."""
+    _case(device, B, N, P, H, G, dtype)
+
+
 def test_heads_modules_use_the_kernels(device):
     """PoM / PoMRoPE with n_sel_heads > 1 gate through pom_gate_heads_* (the
     fused layer and the unfused route both call gate_heads_forward)."""
