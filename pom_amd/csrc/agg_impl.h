@@ -687,12 +687,12 @@ static __global__ void __launch_bounds__(kThreads) coeff_grad_finalize(const flo
   const int64_t stride = (int64_t)K * P;
   float s = 0.0f;
   int64_t r = 0;
-  for (; r + 8 <= rows; r += 8) {   // eight loads in flight, summed in row order
-    float v[8];
+  for (; r + 16 <= rows; r += 16) {   // sixteen loads in flight, summed in row order
+    float v[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) v[q] = src[(r + q) * stride];
+    for (int q = 0; q < 16; ++q) v[q] = src[(r + q) * stride];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) s += v[q];
+    for (int q = 0; q < 16; ++q) s += v[q];
   }
   for (; r < rows; ++r) s += src[r * stride];
   param_set(gc, c * K + j, s);

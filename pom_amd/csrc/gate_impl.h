@@ -330,8 +330,17 @@ static __global__ void __launch_bounds__(kThreads) gate_bwd_finalize(const GateP
   if (!per_token && idx < p.B * p.P) {
     const int64_t b = idx / p.P, c = idx - b * p.P;
     for (int64_t f = 0; f < p.g.F; ++f) {
+      const float* src = p.part_h + (b * nch + f * cpf) * p.P + c;
       float s = 0.0f;
-      for (int64_t k = 0; k < cpf; ++k) s += p.part_h[(b * nch + f * cpf + k) * p.P + c];
+      int64_t k = 0;
+      for (; k + 4 <= cpf; k += 4) {   // four loads in flight, summed in chunk order
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = src[(k + q) * p.P];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s += v[q];
+      }
+      for (; k < cpf; ++k) s += src[k * p.P];
       p.dhagg[(b * p.g.F + f) * p.P + c] = s;
     }
   }
@@ -339,12 +348,12 @@ static __global__ void __launch_bounds__(kThreads) gate_bwd_finalize(const GateP
     const int64_t rows = p.B * nch;
     float s = 0.0f;
     int64_t r = 0;
-    for (; r + 8 <= rows; r += 8) {   // eight loads in flight, summed in row order
-      float v[8];
+    for (; r + 16 <= rows; r += 16) {   // sixteen loads in flight, summed in row order
+      float v[16];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = p.part_b[(r + q) * p.P + idx];
+      for (int q = 0; q < 16; ++q) v[q] = p.part_b[(r + q) * p.P + idx];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) s += v[q];
+      for (int q = 0; q < 16; ++q) s += v[q];
     }
     for (; r < rows; ++r) s += p.part_b[r * p.P + idx];
     param_set(p.dbias, idx, s);
