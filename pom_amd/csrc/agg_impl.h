@@ -392,21 +392,35 @@ __global__ void __launch_bounds__(kThreads) agg_fwd_finalize(const AggParams p) 
   bool have = p.carry != nullptr;
   float h = have ? to_f32<T>(reinterpret_cast<const T*>(p.carry)[b * p.P + c]) : 0.0f;
   float n = (float)p.n_past;
-  for (int64_t f = 0; f < F; ++f) {
-    float s = 0.0f;
-    for (int64_t k = 0; k < cpf; ++k) s += part[(f * cpf + k) * p.P];
-    const float m = MASKED ? (cnt != 0.0f ? s / cnt : 0.0f) : s / (float)p.g.L;
-    if (!recur) {
-      out[0] = from_f32<T>(m);
-      return;
+  constexpr int FB = 8;   // frames whose partial loads are issued together
+  for (int64_t f0 = 0; f0 < F; f0 += FB) {
+    float sf[FB];
+#pragma unroll
+    for (int q = 0; q < FB; ++q) sf[q] = 0.0f;
+    for (int64_t k = 0; k < cpf; ++k) {   // each frame's chunks summed in chunk order
+      float v[FB];
+#pragma unroll
+      for (int q = 0; q < FB; ++q) v[q] = f0 + q < F ? part[((f0 + q) * cpf + k) * p.P] : 0.0f;
+#pragma unroll
+      for (int q = 0; q < FB; ++q) sf[q] += v[q];
     }
-    // The per-frame mean is a tensor of the element type in the reference
-    // (pom/pom_triton.py:348) before it enters the recurrence.
-    const float mt = round_to<T>(m);
-    h = have ? running_mean_step<T>(h, mt, n) : mt;
-    have = true;
-    out[f * p.P] = from_f32<T>(h);
-    n += 1.0f;
+#pragma unroll
+    for (int q = 0; q < FB; ++q) {
+      const int64_t f = f0 + q;
+      if (f >= F) break;
+      const float m = MASKED ? (cnt != 0.0f ? sf[q] / cnt : 0.0f) : sf[q] / (float)p.g.L;
+      if (!recur) {
+        out[0] = from_f32<T>(m);
+        return;
+      }
+      // The per-frame mean is a tensor of the element type in the reference
+      // (pom/pom_triton.py:348) before it enters the recurrence.
+      const float mt = round_to<T>(m);
+      h = have ? running_mean_step<T>(h, mt, n) : mt;
+      have = true;
+      out[f * p.P] = from_f32<T>(h);
+      n += 1.0f;
+    }
   }
 }
 
@@ -419,10 +433,19 @@ static __global__ void __launch_bounds__(kThreads) agg_frame_weights(const AggPa
   if (idx >= p.B * p.P) return;
   const int64_t b = idx / p.P, c = idx - b * p.P;
   const int64_t F = p.g.F;
+  constexpr int FB = 8;   // frames whose loads are issued together (suffix order kept)
   float s = 0.0f;
-  for (int64_t f = F - 1; f >= 0; --f) {
-    s += p.go[(b * F + f) * p.P + c] / ((float)(p.n_past + f) + 1.0f);
-    wf[(b * F + f) * p.P + c] = s / (float)p.g.L;
+  for (int64_t f1 = F - 1; f1 >= 0; f1 -= FB) {
+    float v[FB];
+#pragma unroll
+    for (int q = 0; q < FB; ++q) v[q] = f1 - q >= 0 ? p.go[(b * F + f1 - q) * p.P + c] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < FB; ++q) {
+      const int64_t f = f1 - q;
+      if (f < 0) break;
+      s += v[q] / ((float)(p.n_past + f) + 1.0f);
+      wf[(b * F + f) * p.P + c] = s / (float)p.g.L;
+    }
   }
 }
 

@@ -329,19 +329,22 @@ static __global__ void __launch_bounds__(kThreads) gate_bwd_finalize(const GateP
   const int64_t nch = p.g.nch, cpf = p.g.cpf;
   if (!per_token && idx < p.B * p.P) {
     const int64_t b = idx / p.P, c = idx - b * p.P;
-    for (int64_t f = 0; f < p.g.F; ++f) {
-      const float* src = p.part_h + (b * nch + f * cpf) * p.P + c;
-      float s = 0.0f;
-      int64_t k = 0;
-      for (; k + 4 <= cpf; k += 4) {   // four loads in flight, summed in chunk order
-        float v[4];
+    constexpr int FB = 8;   // frames whose chunk loads are issued together
+    for (int64_t f0 = 0; f0 < p.g.F; f0 += FB) {
+      float sf[FB];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = src[(k + q) * p.P];
+      for (int q = 0; q < FB; ++q) sf[q] = 0.0f;
+      for (int64_t k = 0; k < cpf; ++k) {   // each frame's chunks summed in chunk order
+        float v[FB];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) s += v[q];
+        for (int q = 0; q < FB; ++q)
+          v[q] = f0 + q < p.g.F ? p.part_h[(b * nch + (f0 + q) * cpf + k) * p.P + c] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < FB; ++q) sf[q] += v[q];
       }
-      for (; k < cpf; ++k) s += src[k * p.P];
-      p.dhagg[(b * p.g.F + f) * p.P + c] = s;
+#pragma unroll
+      for (int q = 0; q < FB; ++q)
+        if (f0 + q < p.g.F) p.dhagg[(b * p.g.F + f0 + q) * p.P + c] = sf[q];
     }
   }
   if (p.dbias.ptr && idx < p.P) {
