@@ -28,18 +28,23 @@ static __global__ void __launch_bounds__(kThreads) chunk_exclusive_scan(float* _
   if (idx >= B * P) return;
   const int64_t b = idx / P, c = idx - b * P;
   float* base = cs + b * nch * P + c;
+  // eight chunks loaded before any is rewritten (in place: the loads would
+  // otherwise each wait for the previous store), then scanned in order
+  constexpr int KB = 8;
   float run = 0.0f;
-  if (!reverse) {
-    for (int64_t k = 0; k < nch; ++k) {
-      const float v = base[k * P];
-      base[k * P] = run;
-      run += v;
+  for (int64_t j0 = 0; j0 < nch; j0 += KB) {
+    float v[KB];
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      const int64_t k = reverse ? nch - 1 - (j0 + q) : j0 + q;
+      v[q] = j0 + q < nch ? base[k * P] : 0.0f;
     }
-  } else {
-    for (int64_t k = nch - 1; k >= 0; --k) {
-      const float v = base[k * P];
+#pragma unroll
+    for (int q = 0; q < KB; ++q) {
+      if (j0 + q >= nch) break;
+      const int64_t k = reverse ? nch - 1 - (j0 + q) : j0 + q;
       base[k * P] = run;
-      run += v;
+      run += v[q];
     }
   }
 }
