@@ -271,14 +271,11 @@ int setup_agg(pom::AggParams& p, int dtype, int param_dtype, int64_t B, int64_t 
 }
 
 // Token-causal scan geometry on top of setup_agg (which saw frame_len == 1).
-void setup_scan(const pom::AggParams& a, pom::ScanParams& s, pom::AggParams& sums) {
+void setup_scan(const pom::AggParams& a, pom::ScanParams& s) {
   s.dtype = a.dtype; s.mode = a.mode; s.K = a.K; s.cpt = a.g.cpt; s.nvec = a.g.nvec;
   s.B = a.B; s.N = a.N; s.P = a.P;
   scan_chunks(a.B, a.N, a.g.nvec, s.RC, s.nch);
   s.x = a.x; s.sxb = a.sxb; s.sxn = a.sxn; s.coeff = a.coeff; s.rope = a.rope;
-  sums = a;
-  sums.g.L = a.N; sums.g.F = 1; sums.g.RC = s.RC; sums.g.cpf = s.nch; sums.g.nch = s.nch;
-  sums.direct = 0;
 }
 
 size_t agg_ws_bytes(int64_t B, int64_t N, int64_t P, int K, int64_t frame_len, bool bwd) {
@@ -583,12 +580,10 @@ int pom_agg_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int
   Carve c{static_cast<char*>(workspace), 0};
   if (frame_len == 1 && N > 1) {
     pom::ScanParams s;
-    pom::AggParams sums;
-    setup_scan(p, s, sums);
+    setup_scan(p, s);
     s.out = out;
     s.csum = c.take<float>(B * s.nch * P);
-    sums.part = s.csum;
-    return hip_status(by_dtype(dtype, [&](auto t) { return pom::scan_fwd_t<decltype(t)>(sums, s, st); }),
+    return hip_status(by_dtype(dtype, [&](auto t) { return pom::scan_fwd_t<decltype(t)>(s, st); }),
                       "pom_agg_fwd (token-causal) launch");
   }
   p.direct = (p.g.nch == 1 && p.g.F == 1 && !carry) ? 1 : 0;
@@ -623,8 +618,7 @@ int pom_agg_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int
   Carve c{static_cast<char*>(workspace), 0};
   if (frame_len == 1 && N > 1) {
     pom::ScanParams s;
-    pom::AggParams sums;
-    setup_scan(p, s, sums);
+    setup_scan(p, s);
     s.go = grad_out;
     s.gx = grad_x->data; s.sgb = grad_x->stride_b; s.sgn = grad_x->stride_n;
     s.gc = {grad_coeff, param_dtype};

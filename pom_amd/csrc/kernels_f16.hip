@@ -8,7 +8,7 @@
 namespace pom {
 template hipError_t agg_fwd_t<__half>(const AggParams&, hipStream_t);
 template hipError_t agg_bwd_t<__half>(const AggParams&, hipStream_t);
-template hipError_t scan_fwd_t<__half>(const AggParams&, const ScanParams&, hipStream_t);
+template hipError_t scan_fwd_t<__half>(const ScanParams&, hipStream_t);
 template hipError_t scan_bwd_t<__half>(const ScanParams&, hipStream_t);
 template hipError_t gate_fwd_t<__half>(const GateParams&, int, hipStream_t);
 template hipError_t gate_bwd_t<__half>(const GateParams&, int, hipStream_t);

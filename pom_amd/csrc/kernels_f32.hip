@@ -8,7 +8,7 @@
 namespace pom {
 template hipError_t agg_fwd_t<float>(const AggParams&, hipStream_t);
 template hipError_t agg_bwd_t<float>(const AggParams&, hipStream_t);
-template hipError_t scan_fwd_t<float>(const AggParams&, const ScanParams&, hipStream_t);
+template hipError_t scan_fwd_t<float>(const ScanParams&, hipStream_t);
 template hipError_t scan_bwd_t<float>(const ScanParams&, hipStream_t);
 template hipError_t gate_fwd_t<float>(const GateParams&, int, hipStream_t);
 template hipError_t gate_bwd_t<float>(const GateParams&, int, hipStream_t);

@@ -146,7 +146,7 @@ struct ScanParams {
   float* part = nullptr;          // (B, nch, K, P) backward coefficient partials
 };
 
-template <typename T> hipError_t scan_fwd_t(const AggParams& chunk_sums, const ScanParams& p, hipStream_t st);
+template <typename T> hipError_t scan_fwd_t(const ScanParams& p, hipStream_t st);
 template <typename T> hipError_t scan_bwd_t(const ScanParams& p, hipStream_t st);
 
 // Gating: sh = rot(hardsigmoid(y_s + bias)) * hagg[group(token)]

@@ -49,7 +49,9 @@ static __global__ void __launch_bounds__(kThreads) chunk_exclusive_scan(float* _
   }
 }
 
-template <typename T, int CPT, int KM, int MODE>
+// SUMS: the first pass, which only sums each chunk's (rotated) features into
+// csum, in the same thread layout as the scan itself.
+template <typename T, int CPT, int KM, int MODE, bool SUMS>
 __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanParams p) {
   using Map = LaneMap<CPT, MODE>;
   constexpr int CPT2 = Map::CPT2;
@@ -73,7 +75,7 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanParams p) 
     for (int i = 0; i < CPT2; ++i) {
 #pragma unroll
       for (int j = 0; j < KM; ++j) c[i][j] = j < p.K ? flat[i * KM + j] : 0.0f;
-      acc[i] = pre[map.chan(i)];
+      acc[i] = SUMS ? 0.0f : pre[map.chan(i)];
     }
   }
   const int64_t rbeg = chunk * p.RC;
@@ -108,17 +110,24 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanParams p) 
           o1[i] = acc[i] / cnt;
           o2[i] = acc[CPT + i] / cnt;
         }
-        VecIO<T, CPT>::store(ob + n * p.P + map.c1, o1);
-        VecIO<T, CPT>::store(ob + n * p.P + map.c2, o2);
+        if constexpr (!SUMS) {
+          VecIO<T, CPT>::store(ob + n * p.P + map.c1, o1);
+          VecIO<T, CPT>::store(ob + n * p.P + map.c2, o2);
+        }
       } else {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
           acc[i] += poly<KM>(act(v1[u].get(i)), c[i]);
           o1[i] = acc[i] / cnt;
         }
-        VecIO<T, CPT>::store(ob + n * p.P + map.c1, o1);
+        if constexpr (!SUMS) VecIO<T, CPT>::store(ob + n * p.P + map.c1, o1);
       }
     }
+  }
+  if constexpr (SUMS) {
+    float* cs = p.csum + (b * p.nch + chunk) * p.P;
+#pragma unroll
+    for (int i = 0; i < CPT2; ++i) cs[map.chan(i)] = acc[i];
   }
 }
 
@@ -235,13 +244,19 @@ __global__ void __launch_bounds__(kThreads) scan_bwd_kernel(const ScanParams p) 
       if (j < p.K) part[j * p.P + map.chan(i)] = g[i][j];
 }
 
-template <typename T, int CPT, int KM>
+template <typename T, int CPT, int KM, bool SUMS>
 hipError_t scan_fwd_mode(const ScanParams& p, hipStream_t st) {
   const dim3 grid((unsigned)((p.nvec + kThreads - 1) / kThreads), (unsigned)p.nch, (unsigned)p.B);
   switch (p.mode) {
-    case MODE_PLAIN: hipLaunchKernelGGL((scan_fwd_kernel<T, CPT, KM, MODE_PLAIN>), grid, dim3(kThreads), 0, st, p); break;
-    case MODE_ROPE1D: hipLaunchKernelGGL((scan_fwd_kernel<T, CPT, KM, MODE_ROPE1D>), grid, dim3(kThreads), 0, st, p); break;
-    case MODE_ROPE2D: hipLaunchKernelGGL((scan_fwd_kernel<T, CPT, KM, MODE_ROPE2D>), grid, dim3(kThreads), 0, st, p); break;
+    case MODE_PLAIN:
+      hipLaunchKernelGGL((scan_fwd_kernel<T, CPT, KM, MODE_PLAIN, SUMS>), grid, dim3(kThreads), 0, st, p);
+      break;
+    case MODE_ROPE1D:
+      hipLaunchKernelGGL((scan_fwd_kernel<T, CPT, KM, MODE_ROPE1D, SUMS>), grid, dim3(kThreads), 0, st, p);
+      break;
+    case MODE_ROPE2D:
+      hipLaunchKernelGGL((scan_fwd_kernel<T, CPT, KM, MODE_ROPE2D, SUMS>), grid, dim3(kThreads), 0, st, p);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -260,8 +275,13 @@ hipError_t scan_bwd_mode(const ScanParams& p, hipStream_t st) {
 }
 
 template <typename T, int CPT>
+hipError_t scan_sums_cpt(const ScanParams& p, hipStream_t st) {
+  POM_K_SWITCH(p.K, return (scan_fwd_mode<T, CPT, KM, true>(p, st)))
+}
+
+template <typename T, int CPT>
 hipError_t scan_fwd_cpt(const ScanParams& p, hipStream_t st) {
-  POM_K_SWITCH(p.K, return (scan_fwd_mode<T, CPT, KM>(p, st)))
+  POM_K_SWITCH(p.K, return (scan_fwd_mode<T, CPT, KM, false>(p, st)))
 }
 
 template <typename T, int CPT>
@@ -270,8 +290,11 @@ hipError_t scan_bwd_cpt(const ScanParams& p, hipStream_t st) {
 }
 
 template <typename T>
-hipError_t scan_fwd_t(const AggParams& sums, const ScanParams& p, hipStream_t st) {
-  if (hipError_t e = agg_fwd_chunks<T>(sums, st)) return e;
+hipError_t scan_fwd_t(const ScanParams& p, hipStream_t st) {
+  {
+    auto sums = [&]() -> hipError_t { POM_CPT_SWITCH(T, p.cpt, scan_sums_cpt, p, st) };
+    if (hipError_t e = sums()) return e;
+  }
   hipLaunchKernelGGL(chunk_exclusive_scan, flat_grid(p.B * p.P), dim3(kThreads), 0, st, p.csum, p.B, p.nch, p.P, 0);
   if (hipError_t e = hipGetLastError()) return e;
   POM_CPT_SWITCH(T, p.cpt, scan_fwd_cpt, p, st)
