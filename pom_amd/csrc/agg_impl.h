@@ -700,25 +700,48 @@ agg_bwd_chunk_w3(const AggParams p) {
   agg_bwd_body<T, CPT, KM, MODE, TR>(p);
 }
 
-// grad_coeff[c, j] = sum over (batch row, chunk) of the partials, fixed order.
+// grad_coeff[c, j] = sum over the rows (batch row, chunk) of the partials.
+// A workgroup owns 64 outputs.  From 64 rows on, each of its four waves sums
+// a quarter of the rows (sixteen loads in flight, in row order) and the
+// quarters are added in a fixed order, so a long row list costs a quarter of
+// the round trips; shorter lists are summed by one wave in row order.
+constexpr int kGcOut = kThreads / 4;   // outputs per workgroup (one wave per quarter)
+
 static __global__ void __launch_bounds__(kThreads) coeff_grad_finalize(const float* __restrict__ part, int64_t rows,
                                                                 int64_t P, int K, ParamOut gc) {
-  const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  if (idx >= P * K) return;
-  const int64_t j = idx / P, c = idx - j * P;
+  __shared__ float red[kThreads];
+  const int o = threadIdx.x % kGcOut, qtr = threadIdx.x / kGcOut;
+  const int64_t idx = (int64_t)blockIdx.x * kGcOut + o;
+  const bool live = idx < P * K;
+  const int64_t j = live ? idx / P : 0, c = live ? idx - j * P : 0;
   const float* src = part + j * P + c;
   const int64_t stride = (int64_t)K * P;
+  const int nq = rows >= 64 ? 4 : 1;
+  const int64_t per = (rows + nq - 1) / nq, r0 = qtr * per, r1 = r0 + per < rows ? r0 + per : rows;
   float s = 0.0f;
-  int64_t r = 0;
-  for (; r + 16 <= rows; r += 16) {   // sixteen loads in flight, summed in row order
-    float v[16];
+  if (live && qtr < nq) {
+    int64_t r = r0;
+    for (; r + 16 <= r1; r += 16) {
+      float v[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) v[q] = src[(r + q) * stride];
+      for (int q = 0; q < 16; ++q) v[q] = src[(r + q) * stride];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) s += v[q];
+      for (int q = 0; q < 16; ++q) s += v[q];
+    }
+    for (; r < r1; ++r) s += src[r * stride];
   }
-  for (; r < rows; ++r) s += src[r * stride];
-  param_set(gc, c * K + j, s);
+  red[threadIdx.x] = s;
+  __syncthreads();
+  if (qtr == 0 && live)
+    param_set(gc, c * K + j,
+              nq == 1 ? red[o] : ((red[o] + red[kGcOut + o]) + red[2 * kGcOut + o]) + red[3 * kGcOut + o]);
+}
+
+inline hipError_t launch_coeff_grad_finalize(const float* part, int64_t rows, int64_t P, int K, ParamOut gc,
+                                             hipStream_t st) {
+  hipLaunchKernelGGL(coeff_grad_finalize, dim3((unsigned)((P * K + kGcOut - 1) / kGcOut)), dim3(kThreads), 0, st,
+                     part, rows, P, K, gc);
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -847,9 +870,7 @@ hipError_t agg_bwd_t(const AggParams& p, hipStream_t st) {
     if (hipError_t e = hipGetLastError()) return e;
   }
   if (hipError_t e = agg_bwd_chunks<T>(p, st)) return e;
-  hipLaunchKernelGGL(coeff_grad_finalize, flat_grid(p.P * p.K), dim3(kThreads), 0, st, p.part,
-                     p.B * p.g.nch, p.P, p.K, p.gc);
-  return hipGetLastError();
+  return launch_coeff_grad_finalize(p.part, p.B * p.g.nch, p.P, p.K, p.gc, st);
 }
 
 }  // namespace pom

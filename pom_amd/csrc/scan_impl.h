@@ -317,9 +317,7 @@ hipError_t scan_bwd_t(const ScanParams& p, hipStream_t st) {
     e = run();
   }
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(coeff_grad_finalize, flat_grid(p.P * p.K), dim3(kThreads), 0, st, p.part, p.B * p.nch, p.P,
-                     p.K, p.gc);
-  return hipGetLastError();
+  return launch_coeff_grad_finalize(p.part, p.B * p.nch, p.P, p.K, p.gc, st);
 }
 
 }  // namespace pom
