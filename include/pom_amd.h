@@ -72,7 +72,10 @@ typedef struct pom_tview {
  *   2-D: cos0/sin0 rows (rows0, P/4), cos1/sin1 columns (rows1, P/4),
  *        pos[n * pos_stride + 0] = row, pos[n * pos_stride + 1] = column
  *                                                               (pom/pom_rope.py:120-149, :183-235)
- * Positions outside [0, rows) are clamped to the table. */
+ * A position p in [-rows, 0) selects table row p + rows, as torch's indexing
+ * of the tables does; positions outside [-rows, rows) are clamped to the
+ * table (the reference raises on them; the Python host rejects them where it
+ * can check without a device sync). */
 typedef struct pom_rope {
   int kind;                 /* pom_rope_kind */
   const float* cos0;

@@ -25,6 +25,7 @@ Pinning (how each function is checked, see tests/test_oracle.py):
                                 identity; rotation preserves pair norms
   PoM / PoMRoPE composition     golden fixtures written by the reference itself
                                 (tests/golden/make_golden.py)
+  ar_forward                    golden fixtures of PoM.ar_forward + reset
 """
 from __future__ import annotations
 
@@ -42,7 +43,7 @@ __all__ = [
     "hardsigmoid", "precompute_freqs_1d", "precompute_freqs_2d",
     "apply_rope_1d", "apply_rope_2d", "OracleParams", "init_params",
     "get_h_s", "pom_forward", "state_forward", "rope_forward",
-    "block_causal_dense_mask", "running_mean_frames",
+    "block_causal_dense_mask", "running_mean_frames", "ar_forward",
 ]
 
 
@@ -352,6 +353,15 @@ def state_forward(prm: OracleParams, xq: torch.Tensor, xc: Optional[torch.Tensor
         h, n_past = h_cur, 0
     out = _out_proj(prm, selection(s, h, prm.n_sel_heads))
     return out, {"h": h, "n": n_past + n_cur}
+
+
+def ar_forward(prm: OracleParams, xq: torch.Tensor, state: dict) -> Tuple[torch.Tensor, dict]:
+    """PoM.ar_forward — pom/pom.py:264-275: no aggregation; the gate multiplies
+    the raw projected context token by token, 'n' advances by T."""
+    t = xq.shape[1]
+    h, s = get_h_s(prm, xq, xq, True)
+    out = _out_proj(prm, selection(s, h, prm.n_sel_heads))
+    return out, {"max_len": state["max_len"], "h": h, "n": state["n"] + t}
 
 
 def running_mean_frames(means: torch.Tensor, dtype, carry: Optional[torch.Tensor] = None,

@@ -188,16 +188,46 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
         return buf
 
 
+# Parameter-derived copies (fp32 coefficient / bias copies, transposed and
+# padded weights, fp32 RoPE tables) are rebuilt on every call by default.  A
+# cache keyed on the tensor's identity, storage pointer and version counter is
+# opt-in (set_derived_cache(True) or POM_AMD_CACHE_DERIVED=1): an in-place
+# write through ``p.data`` does not bump the version counter, so with the
+# cache on, such writes (EMA swaps, clamps through .data) must be followed by
+# invalidate_derived().
+_cache_on = os.environ.get("POM_AMD_CACHE_DERIVED", "0") == "1"
+_derived_caches: list = []
+
+
+def set_derived_cache(enabled: bool) -> None:
+    """Turn the parameter-derived copy cache on or off (dropping its entries)."""
+    global _cache_on
+    _cache_on = bool(enabled)
+    invalidate_derived()
+
+
+def derived_cache_enabled() -> bool:
+    return _cache_on
+
+
+def invalidate_derived() -> None:
+    """Drop every cached parameter-derived copy."""
+    for c in _derived_caches:
+        c.clear()
+
+
 def derived(cache: dict, t: "torch.Tensor", make):
-    """``make(t)``, kept while that same tensor object is alive and unchanged
-    (identity, storage pointer and version counter), so a parameter's derived
-    copy is not rebuilt per call while the parameter does not change.  Keyed
-    by object identity: a freed tensor's address or id reused by a new tensor
-    can never hit a stale copy.  Under stream capture the copy is always
-    rebuilt, so a captured graph recomputes it on every replay (a replay runs
-    no Python and would otherwise keep the capture-time copy)."""
-    if torch.cuda.is_current_stream_capturing():
+    """``make(t)``: a copy derived from parameter ``t``.  With the cache on
+    (set_derived_cache), the copy is kept while that same tensor object is
+    alive and unchanged by identity, storage pointer and version counter;
+    keyed by object identity, so a freed tensor's address or id reused by a
+    new tensor can never hit a stale copy.  Under stream capture the copy is
+    always rebuilt, so a captured graph recomputes it on every replay (a replay
+    runs no Python and would otherwise keep the capture-time copy)."""
+    if not _cache_on or (t.is_cuda and torch.cuda.is_current_stream_capturing()):
         return make(t)
+    if not any(c is cache for c in _derived_caches):
+        _derived_caches.append(cache)
     hit = cache.get(id(t))
     if hit is not None:
         ref, version, ptr, c = hit
@@ -224,19 +254,52 @@ def _f32_table(t: torch.Tensor) -> torch.Tensor:
     return derived(_table_cache, t, lambda u: u.detach().float().contiguous())
 
 
+# POM_AMD_CHECK_POSITIONS=1: also range-check RoPE positions that live on the
+# device (one device-to-host synchronisation per RopeSpec).
+_CHECK_DEVICE_POSITIONS = os.environ.get("POM_AMD_CHECK_POSITIONS", "0") == "1"
+
+
+def _check_positions(pos: torch.Tensor, rows) -> None:
+    """Raise IndexError for positions outside [-rows, rows), the range torch's
+    indexing of the tables accepts (pom/pom_rope.py:173-174, :211-212)."""
+    if pos.numel() == 0:
+        return
+    cols = pos.view(-1, 1) if pos.dim() == 1 else pos
+    for j, r in enumerate(rows):
+        lo, hi = int(cols[:, j].min()), int(cols[:, j].max())
+        if lo < -r or hi >= r:
+            raise IndexError(f"RoPE position out of range for a table of {r} rows "
+                             f"(positions span [{lo}, {hi}])")
+
+
 class RopeSpec:
     """Device-side RoPE description: fp32 tables and int64 positions kept alive
-    for as long as the kernels may read them."""
+    for as long as the kernels may read them.
 
-    def __init__(self, kind: int, tables, pos: torch.Tensor):
+    Positions in [-rows, 0) select row p + rows (torch's indexing, done in the
+    kernels' table lookup).  Positions outside [-rows, rows) raise IndexError
+    when they are checked: positions given as a host tensor always are (before
+    the copy to the device), device positions under POM_AMD_CHECK_POSITIONS=1;
+    unchecked ones are clamped to the table by the kernels.  ``n_max``: the
+    positions are known to be arange(n_max) (checked on the host for free).
+    """
+
+    def __init__(self, kind: int, tables, pos: torch.Tensor, device=None, n_max: Optional[int] = None):
         self.kind = kind
         self.tables = [_f32_table(t) for t in tables]
-        self.pos = pos.to(torch.int64).contiguous()
         width = self.tables[0].shape[1]
         for t in self.tables:
             if t.shape[1] != width:
                 raise ValueError("RoPE tables must share their width")
         self.width = width
+        rows = [self.tables[0].shape[0]] if kind == ROPE_1D else [self.tables[0].shape[0], self.tables[2].shape[0]]
+        if n_max is not None:
+            if n_max > min(rows):
+                raise IndexError(f"sequence of {n_max} tokens is longer than the RoPE table ({min(rows)} rows)")
+        elif not pos.is_cuda or _CHECK_DEVICE_POSITIONS:
+            _check_positions(pos, rows)
+        dev = self.tables[0].device if device is None else device
+        self.pos = pos.to(device=dev, dtype=torch.int64).contiguous()
 
     def struct(self) -> PomRope:
         t = self.tables

@@ -82,21 +82,28 @@ __device__ __forceinline__ int64_t slot_chan(int64_t s, int64_t P) {
 }
 
 // cos/sin of token n for CPT consecutive rotation pairs starting at table column
-// tcol.  Positions outside the table are clamped so a bad position can never
-// read outside the table.
+// tcol.  A position p in [-rows, 0) selects row p + rows, as torch's indexing of
+// the tables does (pom/pom_rope.py:173-174, :211-212); positions still outside
+// the table are clamped, so a bad position can never read outside it (the host
+// rejects them where it can check them without a device sync).
 // The two halves of the lookup: the position (a load that the streaming
 // kernels issue together with the step's row loads) and the table entries
 // at that position.
 __device__ __forceinline__ int rope_pos(const RopeTables& t, int table, int64_t n) {
   const int64_t v = t.pos[n * t.pos_sn + table];
-  return v < 0 ? -1 : (v > 0x7fffffff ? 0x7fffffff : (int)v);   // saturated: the table clamp sees the same side
+  // saturated to int: the table lookup sees the same side of the table
+  return v < -0x7fffffff ? -0x7fffffff : (v > 0x7fffffff ? 0x7fffffff : (int)v);
+}
+
+__device__ __forceinline__ int64_t table_row(int64_t pos, int64_t rows) {
+  const int64_t r = pos < 0 ? pos + rows : pos;
+  return r < 0 ? 0 : (r >= rows ? rows - 1 : r);
 }
 
 template <int CPT>
 __device__ __forceinline__ void load_table_at(const RopeTables& t, int table, int pos, int64_t tcol,
                                               float (&cs)[CPT], float (&sn)[CPT]) {
-  const int64_t rows = table ? t.rows1 : t.rows0;
-  const int64_t r = pos < 0 ? 0 : (pos >= rows ? rows - 1 : pos);
+  const int64_t r = table_row(pos, table ? t.rows1 : t.rows0);
   load_f32<CPT>((table ? t.cos1 : t.cos0) + r * t.stride + tcol, cs);
   load_f32<CPT>((table ? t.sin1 : t.sin0) + r * t.stride + tcol, sn);
 }
@@ -104,11 +111,9 @@ __device__ __forceinline__ void load_table_at(const RopeTables& t, int table, in
 template <int CPT>
 __device__ __forceinline__ void load_table(const RopeTables& t, int table, int64_t n, int64_t tcol,
                                            float (&cs)[CPT], float (&sn)[CPT]) {
-  int64_t pos = t.pos[n * t.pos_sn + table];
-  const int64_t rows = table ? t.rows1 : t.rows0;
-  pos = pos < 0 ? 0 : (pos >= rows ? rows - 1 : pos);
-  load_f32<CPT>((table ? t.cos1 : t.cos0) + pos * t.stride + tcol, cs);
-  load_f32<CPT>((table ? t.sin1 : t.sin0) + pos * t.stride + tcol, sn);
+  const int64_t r = table_row(t.pos[n * t.pos_sn + table], table ? t.rows1 : t.rows0);
+  load_f32<CPT>((table ? t.cos1 : t.cos0) + r * t.stride + tcol, cs);
+  load_f32<CPT>((table ? t.sin1 : t.sin0) + r * t.stride + tcol, sn);
 }
 
 }  // namespace pom

@@ -24,11 +24,34 @@ def poly_features(x: torch.Tensor, coeff: torch.Tensor, k: int) -> torch.Tensor:
     return ops.poly_features_hip(x, coeff, k)
 
 
+class _FullMaskMix(torch.autograd.Function):
+    """out = (m @ h) / m.sum(-1): forward and backward as batched GEMMs whose
+    operands are made contiguous first (no transposed views reach bmm)."""
+
+    @staticmethod
+    def forward(ctx, h, m):
+        r = m.sum(dim=2, keepdim=True)
+        out = torch.bmm(m.contiguous(), h.contiguous()) / r
+        ctx.save_for_backward(h, m, r, out)
+        return out
+
+    @staticmethod
+    def backward(ctx, go):
+        h, m, r, out = ctx.saved_tensors
+        g = (go / r).contiguous()
+        gh = gm = None
+        if ctx.needs_input_grad[0]:
+            gh = torch.bmm(m.transpose(1, 2).contiguous(), g)
+        if ctx.needs_input_grad[1]:
+            # d out[i] / d m[i, j] = (h[j] - out[i]) / r[i]
+            gm = torch.bmm(g, h.transpose(1, 2).contiguous()) - (g * out).sum(dim=2, keepdim=True)
+        return gh, gm
+
+
 def full_mask_mix(h: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     """(B, N, P) features, (B, M, N) mask -> (B, M, P) — pom/pom.py:41-45, as
     a batched GEMM (mask @ h) divided by the mask's row sums."""
     m = mask.to(device=h.device, dtype=h.dtype)
     if m.dim() != 3 or m.shape[0] != h.shape[0] or m.shape[2] != h.shape[1]:
         raise ValueError(f"mask must have shape (B, M, N) = ({h.shape[0]}, M, {h.shape[1]}), got {tuple(m.shape)}")
-    out = torch.bmm(m.contiguous(), h.contiguous())
-    return out / m.sum(dim=2, keepdim=True)
+    return _FullMaskMix.apply(h, m)

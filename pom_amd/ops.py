@@ -130,10 +130,9 @@ def transpose(t: torch.Tensor, name: str = "transpose") -> torch.Tensor:
 
 def invalidate_derived() -> None:
     """Drop every cached parameter-derived copy (fp32 coefficients, transposed
-    weights), as an optimizer update of all parameters would."""
-    _f32_cache.clear()
-    _wt_cache.clear()
-    _pad_cache.clear()
+    and padded weights, fp32 RoPE tables), as an optimizer update of all
+    parameters would."""
+    _lib.invalidate_derived()
 
 
 def _transpose_into(src: torch.Tensor, dst: torch.Tensor, name: str) -> None:
@@ -517,11 +516,12 @@ def _rope1d(x: torch.Tensor, freqs_cos, freqs_sin, positions) -> RopeSpec:
     B, N, D = x.shape
     if D % 2 != 0:
         raise ValueError(f"D must be even for RoPE (got {D})")
+    n_max = None
     if positions is None:
-        positions = torch.arange(N, device=x.device, dtype=torch.int64)
+        positions, n_max = torch.arange(N, device=x.device, dtype=torch.int64), N
     if freqs_cos.shape[1] < D // 2:
         raise ValueError("RoPE tables are narrower than D/2")
-    return RopeSpec(_lib.ROPE_1D, [freqs_cos, freqs_sin], positions.to(x.device))
+    return RopeSpec(_lib.ROPE_1D, [freqs_cos, freqs_sin], positions, x.device, n_max)
 
 
 def poly_agg_rope_mean_hip(x, coeff, k, freqs_cos, freqs_sin, positions=None):

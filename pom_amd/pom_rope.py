@@ -99,12 +99,13 @@ class PoMRoPE(PoM):
             if positions_hw.shape != (n, 2):
                 raise ValueError(f"positions_hw must have shape ({n}, 2), got {tuple(positions_hw.shape)}")
             return RopeSpec(_lib.ROPE_2D, [self.row_cos, self.row_sin, self.col_cos, self.col_sin],
-                            positions_hw.to(device))
+                            positions_hw, device)
+        n_max = None
         if positions is None:
-            positions = torch.arange(n, device=device)
+            positions, n_max = torch.arange(n, device=device), n
         if positions.shape != (n,):
             raise ValueError(f"positions must have shape ({n},), got {tuple(positions.shape)}")
-        return RopeSpec(_lib.ROPE_1D, [self.freqs_cos, self.freqs_sin], positions.to(device))
+        return RopeSpec(_lib.ROPE_1D, [self.freqs_cos, self.freqs_sin], positions, device, n_max)
 
     def _spec_heads(self, n: int, positions, positions_hw, device) -> RopeSpec:
         """Device RoPE description for the n_sel_heads-channel gate: the
@@ -120,15 +121,16 @@ class PoMRoPE(PoM):
             st, q = self.head_dim, H // 4
             tabs = [_lib.derived(_HEAD_TABLES, t, lambda u: u[:, ::st][:, :q].float().contiguous())
                     for t in (self.row_cos, self.row_sin, self.col_cos, self.col_sin)]
-            return RopeSpec(_lib.ROPE_2D, tabs, positions_hw.to(device))
+            return RopeSpec(_lib.ROPE_2D, tabs, positions_hw, device)
+        n_max = None
         if positions is None:
-            positions = torch.arange(n, device=device)
+            positions, n_max = torch.arange(n, device=device), n
         if positions.shape != (n,):
             raise ValueError(f"positions must have shape ({n},), got {tuple(positions.shape)}")
         st, half = self.head_dim // 2, H // 2
         tabs = [_lib.derived(_HEAD_TABLES, t, lambda u: u[:, ::st][:, :half].float().contiguous())
                 for t in (self.freqs_cos, self.freqs_sin)]
-        return RopeSpec(_lib.ROPE_1D, tabs, positions.to(device))
+        return RopeSpec(_lib.ROPE_1D, tabs, positions, device, n_max)
 
     def _rope_torch(self, x: torch.Tensor, positions, positions_hw) -> torch.Tensor:
         """PoMRoPE._rope — pom/pom_rope.py:386-437 as tensor ops: full-width

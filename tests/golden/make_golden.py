@@ -151,36 +151,71 @@ def rope_case(P, name, dim, degree, expand, n_sel_heads, B, H, W, rope_2d, mask_
           **_buffers(m), **extra, meta=np.array([dim, degree, expand, n_sel_heads, int(rope_2d), H, W]))
 
 
+def ar_case(P, name, dim, degree, expand, n_sel_heads, n_groups, B, T):
+    """PoM.ar_forward twice from a fresh state, then reset (pom/pom.py:264-280):
+    the per-token gate times the raw projected context, 'n' advancing by T
+    per call, 'max_len' passed through."""
+    torch.manual_seed(0)
+    m = P.PoM(dim, degree, expand, n_groups, n_sel_heads, False)
+    with torch.no_grad():
+        if n_groups == 1:
+            m.se_bias.copy_(torch.randn(m.se_bias.shape, generator=torch.Generator().manual_seed(12)) * 0.5)
+    g = torch.Generator().manual_seed(1)
+    x1 = torch.randn(B, T, dim, generator=g)
+    x2 = torch.randn(B, T, dim, generator=g)
+    state = {"max_len": 64, "h": 0., "n": 0}
+    out1, st1 = m.ar_forward(x1, state)
+    out2, st2 = m.ar_forward(x2, st1)
+    assert st2["max_len"] == 64
+    after = m.reset(dict(st2))
+    _save(name, x1=_np(x1), x2=_np(x2), out1=_np(out1), out2=_np(out2), h1=_np(st1["h"]), h2=_np(st2["h"]),
+          n=np.array([st1["n"], st2["n"]]), reset_n=np.array(after["n"]), reset_h=np.array(float(after["h"])),
+          **_params(m), meta=np.array([dim, degree, expand, n_groups, n_sel_heads, 0]))
+
+
+CASES = [
+    # PoM composition: init order, projections, gating, mean aggregation
+    (pom_case, "pom_mean_f32", (32, 2, 2, 1, 2, 16), {}),
+    (pom_case, "pom_mean_k3_coeff", (32, 3, 2, 1, 2, 16), dict(coeff_std=0.1)),
+    (pom_case, "pom_mean_bias", (24, 2, 3, 1, 2, 12), dict(bias=True, coeff_std=0.1)),
+    (pom_case, "pom_masked", (32, 2, 2, 1, 3, 16), dict(mask_kind="padding", coeff_std=0.1)),
+    (pom_case, "pom_causal", (32, 2, 2, 1, 2, 16), dict(mask_kind="causal", coeff_std=0.1)),
+    (pom_case, "pom_block3d", (32, 2, 2, 1, 2, 16), dict(mask_kind="block3d", coeff_std=0.1)),
+    (pom_case, "pom_heads", (32, 2, 2, 4, 2, 16), dict(coeff_std=0.1)),
+    (pom_case, "pom_groups", (32, 2, 2, 1, 2, 16), dict(n_groups=4, coeff_std=0.1)),
+    # config 1 at its real size (B2 N256 D256 degree 2 expand 2 fp32), seed-0 init
+    (pom_case, "pom_c1", (256, 2, 2, 1, 2, 256), dict(summary=True)),
+    # state_forward: 'n' counts calls, 'h' carried in the input dtype
+    (state_case, "state_f32", (32, 2, 2, 2, 8, 4, torch.float32), {}),
+    (state_case, "state_bf16", (32, 2, 2, 2, 8, 4, torch.bfloat16), {}),
+    # PoMRoPE
+    (rope_case, "rope2d", (16, 2, 2, 1, 2, 4, 4, True), {}),
+    (rope_case, "rope2d_heads", (16, 2, 2, 4, 2, 4, 4, True), {}),
+    (rope_case, "rope1d", (16, 2, 2, 1, 2, 4, 4, False), {}),
+    (rope_case, "rope1d_pos", (16, 2, 2, 1, 2, 4, 4, False),
+     dict(positions=torch.tensor([3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5, 8, 9, 7, 9, 3]))),
+    (rope_case, "rope1d_heads", (16, 2, 2, 4, 2, 4, 4, False), {}),
+    (rope_case, "rope1d_causal", (16, 2, 2, 1, 2, 4, 4, False), dict(mask_kind="causal")),
+    (rope_case, "rope2d_masked", (16, 2, 2, 1, 3, 4, 4, True), dict(mask_kind="padding")),
+    # ar_forward / reset: plain, per-head gate, grouped projection
+    (ar_case, "ar_plain", (32, 2, 2, 1, 1, 2, 8), {}),
+    (ar_case, "ar_heads", (32, 2, 2, 4, 1, 2, 8), {}),
+    (ar_case, "ar_groups", (32, 2, 2, 1, 4, 2, 8), {}),
+]
+
+
 def main():
-    ref = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    """Usage: make_golden.py [reference_dir] [--only=<name prefix> ...]"""
+    args = [a for a in sys.argv[1:] if not a.startswith("--only=")]
+    only = [a[len("--only="):] for a in sys.argv[1:] if a.startswith("--only=")]
+    ref = args[0] if args else "/root/reference"
     os.environ.setdefault("POM_DISABLE_TRITON", "1")
     sys.path.insert(0, ref)
     import pom as P   # the reference package (pure PyTorch route on CPU tensors)
     torch.set_num_threads(4)
-
-    # PoM composition: init order, projections, gating, mean aggregation
-    pom_case(P, "pom_mean_f32", 32, 2, 2, 1, 2, 16)
-    pom_case(P, "pom_mean_k3_coeff", 32, 3, 2, 1, 2, 16, coeff_std=0.1)
-    pom_case(P, "pom_mean_bias", 24, 2, 3, 1, 2, 12, bias=True, coeff_std=0.1)
-    pom_case(P, "pom_masked", 32, 2, 2, 1, 3, 16, mask_kind="padding", coeff_std=0.1)
-    pom_case(P, "pom_causal", 32, 2, 2, 1, 2, 16, mask_kind="causal", coeff_std=0.1)
-    pom_case(P, "pom_block3d", 32, 2, 2, 1, 2, 16, mask_kind="block3d", coeff_std=0.1)
-    pom_case(P, "pom_heads", 32, 2, 2, 4, 2, 16, coeff_std=0.1)
-    pom_case(P, "pom_groups", 32, 2, 2, 1, 2, 16, n_groups=4, coeff_std=0.1)
-    # config 1 at its real size (B2 N256 D256 degree 2 expand 2 fp32), seed-0 init
-    pom_case(P, "pom_c1", 256, 2, 2, 1, 2, 256, summary=True)
-    # state_forward: 'n' counts calls, 'h' carried in the input dtype
-    state_case(P, "state_f32", 32, 2, 2, 2, 8, 4, torch.float32)
-    state_case(P, "state_bf16", 32, 2, 2, 2, 8, 4, torch.bfloat16)
-    # PoMRoPE
-    rope_case(P, "rope2d", 16, 2, 2, 1, 2, 4, 4, True)
-    rope_case(P, "rope2d_heads", 16, 2, 2, 4, 2, 4, 4, True)
-    rope_case(P, "rope1d", 16, 2, 2, 1, 2, 4, 4, False)
-    rope_case(P, "rope1d_pos", 16, 2, 2, 1, 2, 4, 4, False, positions=torch.tensor(
-        [3, 1, 4, 1, 5, 9, 2, 6, 5, 3, 5, 8, 9, 7, 9, 3]))
-    rope_case(P, "rope1d_heads", 16, 2, 2, 4, 2, 4, 4, False)
-    rope_case(P, "rope1d_causal", 16, 2, 2, 1, 2, 4, 4, False, mask_kind="causal")
-    rope_case(P, "rope2d_masked", 16, 2, 2, 1, 3, 4, 4, True, mask_kind="padding")
+    for fn, name, a, kw in CASES:
+        if not only or any(name.startswith(o) for o in only):
+            fn(P, name, *a, **kw)
 
 
 if __name__ == "__main__":

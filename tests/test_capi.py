@@ -257,3 +257,54 @@ def test_features_validation_before_launch(lib):
     rc = lib.pom_features_bwd(1, 1, 2, 64, 32, 2, x, ctypes.c_void_p(512), out, out, ctypes.c_void_p(1024),
                               ctypes.c_void_p(1 << 20), need - 1, None)
     assert rc == _lib.POM_ERR_WORKSPACE
+
+
+def test_derived_copies_rebuilt_by_default_and_cache_opt_in(monkeypatch):
+    """Parameter-derived copies are rebuilt on every call unless the cache is
+    turned on; with it on, a write through .data (which leaves the version
+    counter alone) is not seen until invalidate_derived()."""
+    from pom_amd import _lib, ops
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    cache = {}
+    p = torch.nn.Parameter(torch.zeros(4))
+    make = lambda t: t.detach().clone() + 1
+    assert not _lib.derived_cache_enabled()
+    assert torch.equal(_lib.derived(cache, p, make), torch.ones(4))
+    p.data.add_(1)                                   # no version bump
+    assert torch.equal(_lib.derived(cache, p, make), torch.full((4,), 2.0))
+    try:
+        _lib.set_derived_cache(True)
+        a = _lib.derived(cache, p, make)
+        assert _lib.derived(cache, p, make) is a     # kept while unchanged
+        p.data.add_(1)
+        assert _lib.derived(cache, p, make) is a     # the documented .data limitation
+        ops.invalidate_derived()
+        b = _lib.derived(cache, p, make)
+        assert torch.equal(b, torch.full((4,), 3.0))
+        with torch.no_grad():
+            p.add_(1)                                # bumps the version counter
+        assert torch.equal(_lib.derived(cache, p, make), torch.full((4,), 4.0))
+    finally:
+        _lib.set_derived_cache(False)
+
+
+def test_rope_positions_checked_on_host():
+    """Host positions must lie in [-rows, rows) (the range torch's indexing of
+    the tables accepts, pom/pom_rope.py:173-174); negatives are passed through
+    for the kernels' p + rows lookup; an arange longer than the table raises."""
+    from pom_amd import _lib
+    fc, fs = torch.ones(8, 4), torch.zeros(8, 4)
+    pos = torch.tensor([-8, -1, 0, 7])
+    spec = _lib.RopeSpec(_lib.ROPE_1D, [fc, fs], pos)
+    assert torch.equal(spec.pos, pos) and spec.pos.dtype == torch.int64
+    for bad in ([8], [-9], [0, 100]):
+        with pytest.raises(IndexError):
+            _lib.RopeSpec(_lib.ROPE_1D, [fc, fs], torch.tensor(bad))
+    with pytest.raises(IndexError):
+        _lib.RopeSpec(_lib.ROPE_1D, [fc, fs], torch.arange(9), n_max=9)
+    rc, rs, cc, cs = torch.ones(4, 2), torch.zeros(4, 2), torch.ones(6, 2), torch.zeros(6, 2)
+    _lib.RopeSpec(_lib.ROPE_2D, [rc, rs, cc, cs], torch.tensor([[3, 5], [-4, -6]]))
+    with pytest.raises(IndexError):
+        _lib.RopeSpec(_lib.ROPE_2D, [rc, rs, cc, cs], torch.tensor([[4, 0]]))   # row table has 4 rows
+    with pytest.raises(IndexError):
+        _lib.RopeSpec(_lib.ROPE_2D, [rc, rs, cc, cs], torch.tensor([[0, 6]]))   # column table has 6 rows

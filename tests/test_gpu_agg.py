@@ -179,9 +179,14 @@ def test_causal(device, B, N, D, K, dtype):
     run_case(device, B, N, D, K, dtype, "causal")
 
 
-def _rope1d(D, N, seed=5, random_pos=False):
+def _rope1d(D, N, seed=5, random_pos=False, negative=False):
     fc, fs = O.precompute_freqs_1d(D, 4 * N)
-    if random_pos:
+    if negative:
+        # positions in [-rows, rows): torch's indexing of the tables wraps the
+        # negative ones to p + rows (pom/pom_rope.py:173-174), so must the kernels
+        pos = torch.randint(-4 * N, 4 * N, (N,), generator=torch.Generator().manual_seed(seed))
+        pos[0], pos[-1] = -4 * N, -1
+    elif random_pos:
         pos = torch.randperm(4 * N, generator=torch.Generator().manual_seed(seed))[:N]
     else:
         pos = torch.arange(N)
@@ -215,6 +220,31 @@ def test_rope1d_mean_bf16(device, B, N, D, K):
 @pytest.mark.parametrize("B,N,D,K", [(1, 16, 32, 2), (2, 64, 64, 4)])
 def test_rope1d_causal(device, B, N, D, K, dtype):
     run_case(device, B, N, D, K, dtype, "causal", rope=_rope1d(D, N))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("kind", ["mean", "causal"])
+def test_rope1d_negative_positions(device, kind, dtype):
+    """Negative positions select table row p + rows, as the reference's
+    freqs_cos[positions] does."""
+    run_case(device, 2, 64, 64, 2, dtype, kind, rope=_rope1d(64, 64, negative=True))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,W,D,K", [(2, 8, 8, 64, 2), (1, 16, 16, 96, 3), (8, 8, 24, 64, 2)])
+def test_rope2d_causal(device, B, H, W, D, K, dtype):
+    """2-D RoPE with the token-causal prefix mean (pom/pom_rope.py:282-285 with
+    the rotation of :406-416): the MODE_ROPE2D chunk sums, scan and backward."""
+    run_case(device, B, H * W, D, K, dtype, "causal", rope=_rope2d(D, H, W))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rope", [False, True])
+def test_causal_partial_scan_batch(device, dtype, rope):
+    """B=8, N=192, D=64: the scan splits each row into 12 chunks of 16 tokens,
+    so the chunk scan runs one full batch of eight chunks and then a partial
+    one, and grad_coeff's finalize sums B * 12 = 96 chunk rows (four waves)."""
+    run_case(device, 8, 192, 64, 2, dtype, "causal", rope=_rope1d(64, 192) if rope else None)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

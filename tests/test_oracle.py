@@ -202,9 +202,24 @@ def test_golden_rope(name):
         assert torch.allclose(fc.double(), rope["freqs_cos"]) and torch.allclose(fs.double(), rope["freqs_sin"])
 
 
+@pytest.mark.parametrize("name", ["ar_plain", "ar_heads", "ar_groups"])
+def test_golden_ar_forward(name):
+    """PoM.ar_forward twice, then reset (pom/pom.py:264-280)."""
+    z = _load(name)
+    prm = _params_from(z)
+    state = {"max_len": 64, "h": 0., "n": 0}
+    out1, st1 = O.ar_forward(prm, _t(z["x1"]), state)
+    out2, st2 = O.ar_forward(prm, _t(z["x2"]), st1)
+    assert _rel(out1, z["out1"]) < 1e-6 and _rel(out2, z["out2"]) < 1e-6
+    assert _rel(st1["h"], z["h1"]) < 1e-6 and _rel(st2["h"], z["h2"]) < 1e-6
+    assert [st1["n"], st2["n"]] == [int(v) for v in z["n"]] == [8, 16]
+    assert st2["max_len"] == 64
+    assert int(z["reset_n"]) == 0 and float(z["reset_h"]) == 0.0
+
+
 def test_golden_files_all_used():
     names = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(GOLDEN, "*.npz")))
-    assert len(names) == 18, names
+    assert len(names) == 21, names
 
 
 # ---------------------------------------------------------------------------
