@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 7
+#define POM_AMD_ABI_VERSION 8
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -132,6 +132,24 @@ int pom_agg_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int
                 const pom_rope* rope,
                 void* out, float* count_out,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free variant of pom_agg_fwd: the same arguments and results,
+ * without the workspace.  No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Its scratch is a static device array of
+ * POM_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU
+ * until the process ends; shapes whose pom_agg_workspace_size (forward) is
+ * larger are rejected with POM_ERR_WORKSPACE before anything is launched.
+ * The call allocates and frees nothing.  Every call on one GPU shares that
+ * GPU's scratch, so calls that may overlap on one GPU (different streams)
+ * race; serialise them, or use pom_agg_fwd with a workspace each. */
+#define POM_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int pom_agg_fwd_noalloc(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K,
+                        const pom_view* x, const void* coeff,
+                        const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
+                        int64_t frame_len, const void* carry, int64_t n_past,
+                        const pom_rope* rope,
+                        void* out, float* count_out, void* stream);
 
 /* Backward.  grad_out: (B, N/frame_len, P) fp32.  count: (B,) fp32 from the
  * forward (masked mode).  grad_x: view written for every token (0 where the

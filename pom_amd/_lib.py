@@ -27,7 +27,8 @@ POM_ERR_DEVICE = 4
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
 MAX_DEGREE = 16
-ABI_VERSION = 7
+ABI_VERSION = 8
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/pom_amd.h declares, with its ctypes signature.
 _c_i64 = ctypes.c_int64
@@ -60,6 +61,8 @@ SIGNATURES = {
     "pom_agg_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_i64, _c_int, _c_int]),
     "pom_agg_fwd": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64, _c_i64,
                              _c_i64, _c_vp, _c_i64, _PR, _c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "pom_agg_fwd_noalloc": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64,
+                                     _c_i64, _c_i64, _c_vp, _c_i64, _PR, _c_vp, _c_vp, _c_vp]),
     "pom_agg_bwd": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _c_vp, _c_i64, _c_i64,
                              _c_vp, _c_i64, _c_i64, _PR, _c_vp, _PV, _PT, _c_vp, _c_vp, _c_size, _c_vp]),
     "pom_gate_workspace_size": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int]),

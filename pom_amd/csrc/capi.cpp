@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <initializer_list>
+#include <mutex>
 #include <string>
 
 #include "../../include/pom_amd.h"
@@ -544,6 +545,41 @@ int setup_features(pom::FeatParams& p, int dtype, int param_dtype, int64_t B, in
 
 }  // namespace
 
+// Device scratch of pom_agg_fwd_noalloc: one copy per GPU, allocated when the
+// code object is loaded on that GPU and held until the process ends.  In host
+// code the name is only a handle; the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is ever passed
+// to a kernel.
+static __device__ __align__(256) unsigned char scratch[POM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device, with that device current).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(POM_ERR_UNSUPPORTED, "device index %d is beyond the %d the static scratch tracks", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+      return hip_status(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(POM_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return POM_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int pom_abi_version(void) { return POM_AMD_ABI_VERSION; }
@@ -591,6 +627,24 @@ int pom_agg_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int
   p.pcnt = c.take<float>(B * p.g.nch);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::agg_fwd_t<decltype(t)>(p, st); }),
                     "pom_agg_fwd launch");
+}
+
+int pom_agg_fwd_noalloc(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x,
+                        const void* coeff, const float* mask, int64_t mask_stride_b, int64_t mask_stride_n,
+                        int64_t frame_len, const void* carry, int64_t n_past, const pom_rope* rope, void* out,
+                        float* count_out, void* stream) {
+  // The scratch size is checked from the shape alone, before anything else.
+  // An invalid shape reports 0 here and is rejected by pom_agg_fwd's checks.
+  const size_t need = pom_agg_workspace_size(dtype, B, N, P, K, frame_len, rope ? rope->kind : POM_ROPE_NONE, 0);
+  if (need > POM_NOALLOC_SCRATCH_BYTES)
+    return fail(POM_ERR_WORKSPACE,
+                "pom_agg_fwd_noalloc: this shape needs %zu bytes of scratch, more than the %zu of the static "
+                "scratch; call pom_agg_fwd with a workspace instead",
+                need, (size_t)POM_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int r = scratch_for_current_device(&ws)) return r;
+  return pom_agg_fwd(dtype, param_dtype, B, N, P, K, x, coeff, mask, mask_stride_b, mask_stride_n, frame_len, carry,
+                     n_past, rope, out, count_out, ws, POM_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int pom_agg_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int K, const pom_view* x,

@@ -259,6 +259,23 @@ def test_features_validation_before_launch(lib):
     assert rc == _lib.POM_ERR_WORKSPACE
 
 
+def test_noalloc_rejects_oversize_shapes_before_any_device_call(lib):
+    """pom_agg_fwd_noalloc checks the shape's scratch need first: the token-causal
+    C4 shape (64 MiB of forward scratch) is refused before anything else."""
+    from pom_amd import _lib
+    need = lib.pom_agg_workspace_size(1, 4, 16384, 4096, 2, 1, 0, 0)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    x = _view(256, 16384 * 4096, 4096)
+    rc = lib.pom_agg_fwd_noalloc(1, 1, 4, 16384, 4096, 2, ctypes.byref(x), ctypes.c_void_p(512), None, 0, 0, 1,
+                                 None, 0, None, ctypes.c_void_p(1024), None, None)
+    assert rc == _lib.POM_ERR_WORKSPACE
+    assert b"static scratch" in lib.pom_last_error()
+    # every baseline configuration's forward fits
+    for B, N, P, K, fl, rk in [(2, 256, 512, 2, 256, 0), (16, 1024, 2304, 2, 1024, 0), (32, 2048, 2048, 3, 2048, 0),
+                               (4, 16384, 4096, 2, 1024, 0), (8, 4096, 3072, 2, 4096, 2)]:
+        assert 0 < lib.pom_agg_workspace_size(1, B, N, P, K, fl, rk, 0) <= _lib.NOALLOC_SCRATCH_BYTES
+
+
 def test_derived_copies_rebuilt_by_default_and_cache_opt_in(monkeypatch):
     """Parameter-derived copies are rebuilt on every call unless the cache is
     turned on; with it on, a write through .data (which leaves the version
