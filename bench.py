@@ -1,8 +1,8 @@
 """PoM layer benchmark on one MI355X: forward + backward tokens/s, per-kernel
 roofline fractions and a CPU baseline, printed as ONE JSON line.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5]
-                  [--no-cpu] [--fwd] [--copy-calib MiB]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5|c2h]
+                  [--sub-configs c3,c4,c5] [--no-cpu] [--no-flush] [--graph]
 
 A step is one forward + backward of one PoM layer over one batch of synthetic
 input that is resident in HBM before the timed region starts (x, upstream
@@ -15,8 +15,22 @@ without them), giving each kernel's average duration; the roofline object
 reports the kernel that takes the most time per step, and "kernels" reports
 all of them.
 
+Roofline fractions are in algorithmic units: the bytes (or flops) the
+operation itself needs per launch.  Kernels that also write a channel-major
+copy of their output for the backward GEMMs report those copy bytes
+separately ("copy_bytes", "frac_with_copies").
+
+Besides the headline configuration, the same JSON line carries one object per
+other baseline configuration ("configs": C3-C5 by default) with its fwd and
+fwd+bwd tokens/s, its dominant-kernel roofline, the streaming / GEMM group
+fractions and its own CPU baseline.  "mall_flushed" repeats the headline step
+with 1 GiB written before every step (the Infinity Cache and L2 cold at the
+layer's start), and times each streaming kernel standalone, back to back
+(warm) and after a 1 GiB write before every launch (cold).
+
 The CPU baseline runs the oracle (a pure-PyTorch restatement of the reference
-path) in fp32 on the host cores on a bounded sample of the same workload.
+path) on the host cores on a bounded sample of the same workload, fp32 and
+bf16, forward and forward + backward.
 """
 from __future__ import annotations
 
@@ -58,7 +72,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--sub-configs", default="c3,c4,c5",
+                    help="comma-separated other configurations measured into the same JSON line ('' for none)")
+    ap.add_argument("--sub-cpu-seconds", type=float, default=6.0, help="CPU baseline budget per sub-config")
+    ap.add_argument("--no-flush", action="store_true", help="skip the MALL-flushed measurements")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="time the steps without per-launch events")
@@ -68,6 +86,10 @@ def parse():
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DB", "WRITE_DB", "COPY_FETCH_DB", "COPY_WRITE_DB"),
                     help="turn four rocprofv3 --pmc databases (FETCH_SIZE and WRITE_SIZE of a bench run and "
                          "of a --copy-calib run) into per-kernel HBM traffic; writes profiles/traffic_<config>.json")
+    ap.add_argument("--pmc-table", nargs="+", metavar=("DB", "COUNTER"),
+                    help="per launch group, the mean of each named counter per dispatch in one rocprofv3 --pmc "
+                         "database of a bench run (e.g. MfmaUtil MfmaFlopsBF16 for the GEMMs); writes "
+                         "profiles/pmc_<config>_<first counter>.json")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="summarise a rocprofv3 --kernel-trace --stats --output-format csv directory "
                          "(run_kernel_stats.csv, run_kernel_trace.csv) of a bench run: per-kernel calls and "
@@ -150,33 +172,33 @@ def kernel_work(cfg, extra):
     # channel-major copies written in the same pass (16-bit training path)
     from pom_amd import ops
     cm = T * P * e if (ops._NT_GEMMS and ops._NT_COPIES == "fused") else 0
+    # name: (bound, algorithmic bytes or flops per launch, channel-major copy bytes written besides)
     w = {
-        "gemm_qc_fwd": ("mfma", 2.0 * T * D * Q),
-        "gemm_ag_fwd": ("mfma", 2.0 * T * P * D),
-        "gemm_ag_dgrad": ("mfma", 2.0 * T * D * P),
-        "gemm_ag_wgrad": ("mfma", 2.0 * T * D * P),
-        "gemm_qc_dgrad": ("mfma", 2.0 * T * Q * D),
-        "gemm_qc_wgrad": ("mfma", 2.0 * T * Q * D),
+        "gemm_qc_fwd": ("mfma", 2.0 * T * D * Q, 0),
+        "gemm_ag_fwd": ("mfma", 2.0 * T * P * D, 0),
+        "gemm_ag_dgrad": ("mfma", 2.0 * T * D * P, 0),
+        "gemm_ag_wgrad": ("mfma", 2.0 * T * D * P, 0),
+        "gemm_qc_dgrad": ("mfma", 2.0 * T * Q * D, 0),
+        "gemm_qc_wgrad": ("mfma", 2.0 * T * Q * D, 0),
         # x read (valid tokens only when masked) + aggregate written
-        "agg_fwd": ("hbm", float(read_tok * P * e + agg_out + mask_b + rope_tab)),
-        # x read for valid tokens, grad_x (and its channel-major copy) written for every token,
-        # fp32 upstream grad read
-        "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + cm + B * G * P * 4 + mask_b)),
-        # y_s read, sh (and sh^T) written, aggregate read
-        "gate_fwd": ("hbm", float(2 * T * P * e + cm + B * G * P * e)),
-        # y_s and dsh read, dy_s (and its channel-major copy) written
-        "gate_bwd": ("hbm", float(3 * T * P * e + cm + B * G * P * 4)),
-        # per-head gate: sh (and sh^T) written (y_s and hagg are H / P wide per token / row)
-        "gate_heads_fwd": ("hbm", float(T * P * e + cm + T * H * e + B * G * P * e)),
+        "agg_fwd": ("hbm", float(read_tok * P * e + agg_out + mask_b + rope_tab), 0),
+        # x read for valid tokens, grad_x written for every token, fp32 upstream grad read
+        "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + B * G * P * 4 + mask_b), cm),
+        # y_s read, sh written, aggregate read
+        "gate_fwd": ("hbm", float(2 * T * P * e + B * G * P * e), cm),
+        # y_s and dsh read, dy_s written, fp32 dhagg written
+        "gate_bwd": ("hbm", float(3 * T * P * e + B * G * P * 4), cm),
+        # per-head gate: sh written (y_s and hagg are H / P wide per token / row)
+        "gate_heads_fwd": ("hbm", float(T * P * e + T * H * e + B * G * P * e), cm),
         # dsh read once, y_s read, dy_s written, fp32 dhagg written
-        "gate_heads_bwd": ("hbm", float(T * P * e + 2 * T * H * e + B * G * P * 4)),
+        "gate_heads_bwd": ("hbm", float(T * P * e + 2 * T * H * e + B * G * P * 4), 0),
         # operand-layout transposes for the backward GEMMs: read + write once
-        "transpose_x": ("hbm", float(2 * T * D * e)),
-        "transpose_sh": ("hbm", float(2 * T * P * e)),
-        "transpose_g": ("hbm", float(2 * T * D * e)),
+        "transpose_x": ("hbm", float(2 * T * D * e), 0),
+        "transpose_sh": ("hbm", float(2 * T * P * e), 0),
+        "transpose_g": ("hbm", float(2 * T * D * e), 0),
         # all of dY, or only its gate part when the streaming kernels write the rest
-        "transpose_dy": ("hbm", float(2 * T * (S if cm else Q) * e)),
-        "transpose_w": ("hbm", float(2 * 2 * P * D * e)),   # W_qc or W_ag: counted as the larger
+        "transpose_dy": ("hbm", float(2 * T * (S if cm else Q) * e), 0),
+        "transpose_w": ("hbm", float(2 * 2 * P * D * e), 0),   # W_qc or W_ag: counted as the larger
     }
     return w
 
@@ -288,6 +310,120 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
     return ms_step, ms_fwd, per, extra, (dominant, live)
 
 
+FLUSH_BYTES = 1 << 30   # 4x the 256 MB Infinity Cache
+
+
+def _flusher(dev):
+    """A 1 GiB fill: evicts the Infinity Cache (MALL) and every XCD's L2."""
+    import torch
+    buf = torch.empty(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+    return lambda: buf.fill_(1.0)
+
+
+def flushed_layer(cfg, steps, warmup):
+    """The fwd+bwd step with 1 GiB written before every step: per-step GPU time
+    from events around the step only (the fill is outside them), and the
+    per-kernel spans of the same steps."""
+    import torch
+    from pom_amd import ops
+    dev = torch.device("cuda:0")
+    x, go, extra = make_inputs(cfg)
+    m = make_module(cfg).to(dev, torch.bfloat16)
+    xd = x.to(dev, torch.bfloat16).requires_grad_(True)
+    god = go.to(dev, torch.bfloat16)
+    fwd = forward_fn(cfg, {k: v.to(dev) for k, v in extra.items()})
+    params = list(m.parameters())
+    flush = _flusher(dev)
+
+    def step():
+        for p in params:
+            p.grad = None
+        xd.grad = None
+        ops.invalidate_derived()
+        fwd(m, xd).backward(god)
+
+    for _ in range(warmup):
+        step()
+    spans = []
+    ops.kernel_timer = []
+    for _ in range(steps):
+        flush()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step()
+        e1.record()
+        spans.append((e0, e1))
+    torch.cuda.synchronize()
+    per = {}
+    for name, a, b in ops.kernel_timer:
+        per.setdefault(name, []).append(a.elapsed_time(b) * 1e-3)
+    ops.kernel_timer = None
+    ms = sum(a.elapsed_time(b) for a, b in spans) / steps
+    return ms, per
+
+
+def stream_kernels_warm_cold(cfg, reps):
+    """The four streaming kernels of the full-width layer, standalone on the
+    layer's operand shapes (Y's h- and s-parts as strided views, channel-major
+    copies as in the training step): mean duration back to back (warm) and
+    with 1 GiB written before every launch (cold: operands come from HBM)."""
+    import torch
+    from pom_amd import ops
+    if cfg["variant"] != "mean" or cfg.get("heads", 1) > 1:
+        return None
+    dev = torch.device("cuda:0")
+    B, N, D, K, E = cfg["B"], cfg["N"], cfg["D"], cfg["K"], cfg["E"]
+    T, P = B * N, E * D
+    W = ops._padded_width(P, P)
+    g = torch.Generator().manual_seed(5)
+    y = torch.randn(T, W, generator=g).to(dev, torch.bfloat16)
+    y3 = y.view(B, N, W)
+    h, ys = y3[..., :P], y3[..., P:2 * P]
+    c = (torch.randn(P, K, generator=g) * 0.05).to(dev, torch.bfloat16)
+    bias = torch.zeros(P, device=dev, dtype=torch.bfloat16)
+    dsh = torch.randn(B, N, P, generator=g).to(dev, torch.bfloat16)
+    dh = torch.randn(B, 1, P, generator=g).to(dev)
+    dy = torch.empty(T, W, device=dev, dtype=torch.bfloat16)
+    dy3 = dy.view(B, N, W)
+    dyt = torch.empty(W, T, device=dev, dtype=torch.bfloat16)
+    sht = torch.empty(P, T, device=dev, dtype=torch.bfloat16)
+    hagg, _ = ops.agg_forward(h, c, K, N)
+    calls = {
+        "agg_fwd": lambda: ops.agg_forward(h, c, K, N),
+        "gate_fwd": lambda: ops.gate_forward(ys, bias, hagg, out_t=sht),
+        "gate_bwd": lambda: ops.gate_backward(ys, bias, hagg, dsh, dy3[..., P:], grad_ys_t=dyt[P:],
+                                              grad_ys_rows=dy[:, P:]),
+        "agg_bwd": lambda: ops.agg_backward(h, c, K, N, dh, dy3[..., :P], grad_x_t=dyt[:P],
+                                            grad_x_rows=dy[:, :P]),
+    }
+    flush = _flusher(dev)
+    work = kernel_work(cfg, {})
+    out = {}
+    for name, call in calls.items():
+        for _ in range(3):
+            call()
+        res = {}
+        for mode in ("warm", "cold"):
+            evs = []
+            for _ in range(reps):
+                if mode == "cold":
+                    flush()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                call()
+                e1.record()
+                evs.append((e0, e1))
+            torch.cuda.synchronize()
+            res[mode] = sum(a.elapsed_time(b) for a, b in evs) / reps * 1e-3
+        _, amount, copy = work[name]
+        out[name] = {"bytes": amount, "copy_bytes": copy,
+                     "warm_us": round(res["warm"] * 1e6, 2), "cold_us": round(res["cold"] * 1e6, 2),
+                     "warm_frac": round(amount / res["warm"] / HBM_PEAK, 4),
+                     "cold_frac": round(amount / res["cold"] / HBM_PEAK, 4),
+                     "cold_frac_with_copies": round((amount + copy) / res["cold"] / HBM_PEAK, 4)}
+    return out
+
+
 def copy_calib(mib: float):
     """A plain device-to-device copy of known size, for counter calibration."""
     import torch
@@ -306,49 +442,91 @@ def copy_calib(mib: float):
 # CPU leg: the oracle, fp32, on the host cores
 # ---------------------------------------------------------------------------
 
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+# Threads of the CPU baseline: every core of the process's affinity mask, up to
+# the 16 host cores one GPU of the measurement boxes is given (the harness
+# sets OMP_NUM_THREADS to that share; more threads would oversubscribe it).
+CPU_THREAD_CAP = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+
+
 def cpu_run(cfg, budget_s: float):
+    """The oracle (pure-PyTorch restatement of the reference path) on a bounded
+    sample of the workload's batch rows: fp32 fwd+bwd (the reported value),
+    fp32 forward, and bf16 fwd+bwd and forward.  1 warm-up, median of 3."""
     import torch
     from oracle import pom_oracle as O
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    affinity = len(os.sched_getaffinity(0))
+    cores = max(1, min(affinity, CPU_THREAD_CAP))
     torch.set_num_threads(cores)
     x, go, extra = make_inputs(cfg)
     torch.manual_seed(0)
     rope2d = True if cfg["variant"] == "rope2d" else None
-    prm = O.init_params(cfg["D"], cfg["K"], cfg["E"], n_sel_heads=cfg.get("heads", 1), rope_2d=rope2d,
-                        max_h=cfg.get("H", 64), max_w=cfg.get("W", 64))
-    for t in (prm.w_qc, prm.se_bias, prm.po_coeff, prm.w_ag):
-        t.requires_grad_(True)
-    # bounded sample: the first batch rows of the workload, as many as the budget allows
+    prm32 = O.init_params(cfg["D"], cfg["K"], cfg["E"], n_sel_heads=cfg.get("heads", 1), rope_2d=rope2d,
+                          max_h=cfg.get("H", 64), max_w=cfg.get("W", 64))
     v = cfg["variant"]
 
-    def run(nb):
-        xs = x[:nb].clone().requires_grad_(True)
-        if v == "mean":
-            out = O.pom_forward(prm, xs)
-        elif v == "masked":
-            out = O.pom_forward(prm, xs, mask=extra["mask"][:nb])
-        elif v == "block":
-            out = O.pom_forward(prm, xs, mask=("block_causal", cfg["frame_len"]))
-        else:
-            out = O.rope_forward(prm, xs, positions_hw=extra["positions_hw"])
-        out.backward(go[:nb])
+    def params(dt):
+        prm = prm32.to(dt)
+        for t in (prm.w_qc, prm.se_bias, prm.po_coeff, prm.w_ag):
+            t.requires_grad_(True)
+        return prm
 
-    nb = 1
+    def run(prm, nb, dt, backward):
+        xs = x[:nb].to(dt).clone().requires_grad_(backward)
+        with torch.set_grad_enabled(backward):
+            if v == "mean":
+                out = O.pom_forward(prm, xs)
+            elif v == "masked":
+                out = O.pom_forward(prm, xs, mask=extra["mask"][:nb])
+            elif v == "block":
+                # the O(N) frame-causal route (the reference's state_forward loop
+                # computes the same per-frame aggregate)
+                out = O.pom_forward(prm, xs, mask=("block_causal", cfg["frame_len"]))
+            else:
+                out = O.rope_forward(prm, xs, positions_hw=extra["positions_hw"])
+            if backward:
+                out.backward(go[:nb].to(dt))
+
+    def timed(prm, nb, dt, backward, reps=3):
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            run(prm, nb, dt, backward)
+            ts.append(time.perf_counter() - t0)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    p32, p16 = params(torch.float32), params(torch.bfloat16)
     t0 = time.perf_counter()
-    run(nb)                                  # warm-up on one batch row
+    run(p32, 1, torch.float32, True)                     # warm-up on one batch row
     t_one = time.perf_counter() - t0
-    nb = max(1, min(cfg["B"], int(budget_s / 3 / max(t_one, 1e-3))))
-    times = []
-    for _ in range(3):
-        s = time.perf_counter()
-        run(nb)
-        times.append(time.perf_counter() - s)
-    times.sort()
-    med = times[1]
+    # share of the budget: fp32 fwd+bwd 1/2, the other three legs the rest
+    nb = max(1, min(cfg["B"], int(budget_s / 2 / 3 / max(t_one, 1e-3))))
     tok = nb * cfg["N"]
-    return {"value": tok / med, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"oracle fp32 layer fwd+bwd on {nb} of {cfg['B']} batch rows ({tok} tokens), "
-                      f"median of 3 after 1 warm-up, torch.set_num_threads({cores})"}
+    med = timed(p32, nb, torch.float32, True)
+    res = {"value": tok / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+           "sample": f"oracle fp32 layer fwd+bwd on {nb} of {cfg['B']} batch rows ({tok} tokens), "
+                     f"median of 3 after 1 warm-up, torch.set_num_threads({cores})",
+           "fwd_value": tok / timed(p32, nb, torch.float32, False),
+           "affinity_cores": affinity, "cpu_model": _cpu_model(),
+           "threads_note": f"min(affinity cores, {CPU_THREAD_CAP}): the host-core share of one GPU on the box"}
+    run(p16, 1, torch.bfloat16, True)                    # bf16 warm-up
+    res["bf16_value"] = tok / timed(p16, nb, torch.bfloat16, True)
+    res["bf16_fwd_value"] = tok / timed(p16, nb, torch.bfloat16, False)
+    for k in ("value", "fwd_value", "bf16_value", "bf16_fwd_value"):
+        res[k] = round(res[k], 1)
+    return res
 
 
 # rocprofv3 kernel names of the launch groups bench.py times
@@ -461,6 +639,38 @@ def pmc_summary(cfg_name, dbs):
     print(json.dumps({"wrote": path, "groups": groups, "fetch_scale": f_scale, "write_scale": w_scale}))
 
 
+def pmc_table(cfg_name, db, counters):
+    """Mean value per dispatch of each counter, per launch group: the layer's
+    streaming kernels by name, the projection GEMMs by dispatch order (the
+    last complete fwd+bwd step).  MfmaUtil (rocprofv3's derived metric,
+    SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x SIMDs, in %) and
+    MfmaFlopsBF16 (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512) give the GEMMs' matrix
+    core utilisation and the flops they executed."""
+    per = {c: _pmc_per_kernel(db, c) for c in counters}
+    out = {"config": cfg_name, "database": db, "counters": counters, "groups": {}}
+    for g, names in KERNEL_NAMES.items():
+        row = {}
+        for c in counters:
+            tot, found = 0.0, False
+            for n in names:
+                cand = [(v[0], v[1]) for k, v in per[c].items() if n in k]
+                if cand:
+                    tot += max(cand)[1]
+                    found = True
+            if found:
+                row[c] = tot
+        if row:
+            out["groups"][g] = row
+    gd = _gemm_dispatches(db)
+    for g, (d, kname) in gd.items():
+        out["groups"][g] = {c: _pmc_dispatch(db, c).get(d) for c in counters}
+        out["groups"][g]["kernel"] = kname
+    path = os.path.join(ROOT, "profiles", f"pmc_{cfg_name}_{counters[0]}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps({"wrote": path, "groups": out["groups"]}))
+
+
 def trace_summary(trace_dir):
     """Table of a kernel-trace run: calls, average us, share of GPU time, kernel
     (library GEMMs labelled with their projection from the dispatch order of
@@ -507,6 +717,96 @@ def traffic_of(cfg_name, group):
         return None
 
 
+def _kernel_table(per, work, steps):
+    kernels = {}
+    for name, durs in per.items():
+        bound, amount, copy = work[name]
+        avg = sum(durs) / len(durs)
+        peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
+        achieved = amount / avg
+        k = {"bound": bound, "avg_us": round(avg * 1e6, 2), "us_per_step": round(sum(durs) / steps * 1e6, 2),
+             "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
+             "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4),
+             "launches_per_step": len(durs) / steps}
+        if copy:
+            k["copy_bytes"] = copy
+            k["frac_with_copies"] = round((amount + copy) / avg / peak, 4)
+        if name in overlapped_groups():
+            k["overlapped"] = True   # span includes waiting for compute units
+        kernels[name] = k
+    return kernels
+
+
+def _groups(kernels, work):
+    agg = [n for n in ("agg_fwd", "agg_bwd", "gate_fwd", "gate_bwd", "gate_heads_fwd", "gate_heads_bwd")
+           if n in kernels]
+    gem = [n for n in kernels if n.startswith("gemm")]
+    t_hbm = sum(kernels[n]["us_per_step"] for n in agg)
+    t_mf = sum(kernels[n]["us_per_step"] for n in gem)
+    b_hbm = sum(work[n][1] for n in agg)
+    c_hbm = sum(work[n][2] for n in agg)
+    f_mf = sum(work[n][1] for n in gem)
+    return {
+        "hip_streaming_kernels": {"us_per_step": round(t_hbm, 2),
+                                  "frac_hbm": round(b_hbm / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None,
+                                  "frac_hbm_with_copies":
+                                      round((b_hbm + c_hbm) / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None},
+        "projection_gemms": {"us_per_step": round(t_mf, 2),
+                             "frac_mfma": round(f_mf / (t_mf * 1e-6) / MFMA_BF16_PEAK, 4) if t_mf else None},
+        "ideal_step_us": round((b_hbm / HBM_PEAK + f_mf / MFMA_BF16_PEAK) * 1e6, 2),
+    }
+
+
+def measure(name, a, headline):
+    """One configuration: GPU step timings, per-kernel table, dominant-kernel
+    roofline, group fractions and the CPU baseline."""
+    import torch
+    cfg = CONFIGS[name]
+    steps = a.steps if headline else min(a.steps, 20)
+    ms_step, ms_fwd, per, extra, (dominant, live) = gpu_run(cfg, steps, a.warmup,
+                                                            not a.no_kernel_timing and not a.graph, a.graph)
+    T = cfg["B"] * cfg["N"]
+    work = kernel_work(cfg, extra)
+    kernels = _kernel_table(per, work, steps)
+    roofline = None
+    if kernels and dominant and live:
+        k = kernels[dominant]
+        bound, amount, copy = work[dominant]
+        avg = sum(live) / len(live)                      # from the timed region's events
+        achieved = amount / avg
+        peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
+        roofline = {"kernel": dominant, "bound": bound,
+                    "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
+                    "peak": 8000.0 if bound == "hbm" else 2500.0, "unit": k["unit"],
+                    "frac": round(achieved / peak, 4), "avg_us": round(avg * 1e6, 2),
+                    "launches_timed": len(live), "traffic": traffic_of(name, dominant)}
+        if copy:
+            roofline["copy_bytes"] = copy
+            roofline["frac_with_copies"] = round((amount + copy) / avg / peak, 4)
+    res = {"workload": cfg["workload"],
+           "config": {"workload": cfg["workload"], "B": cfg["B"], "N": cfg["N"], "D": cfg["D"],
+                      "degree": cfg["K"], "expand": cfg["E"], "tokens_per_step": T},
+           "steps": steps, "ms_per_step": round(ms_step, 4), "value": round(T / (ms_step * 1e-3), 1),
+           "fwd_tokens_per_s": round(T / (ms_fwd * 1e-3), 1) if ms_fwd else None,
+           "ms_fwd": round(ms_fwd, 4) if ms_fwd else None, "roofline": roofline, "kernels": kernels}
+    if cfg.get("heads", 1) > 1:
+        res["config"]["n_sel_heads"] = cfg["heads"]
+    if kernels:
+        res["roofline_groups"] = _groups(kernels, work)
+    if headline and not a.no_flush and not a.graph:
+        ms_fl, per_fl = flushed_layer(cfg, min(steps, 20), a.warmup)
+        k_fl = _kernel_table(per_fl, work, min(steps, 20))
+        res["mall_flushed"] = {
+            "note": "1 GiB written before every step; events around the step only",
+            "ms_per_step": round(ms_fl, 4), "value": round(T / (ms_fl * 1e-3), 1),
+            "kernels": {n: {kk: v[kk] for kk in ("avg_us", "frac") if kk in v} for n, v in k_fl.items()},
+            "streaming_kernels_standalone": stream_kernels_warm_cold(cfg, 20)}
+    torch.cuda.empty_cache()
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_run(cfg, a.cpu_seconds if headline else a.sub_cpu_seconds)
+    return res
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -522,64 +822,28 @@ def main():
     if a.trace_summary:
         trace_summary(a.trace_summary)
         return
-    cfg = CONFIGS[a.config]
-    ms_step, ms_fwd, per, extra, (dominant, live) = gpu_run(cfg, a.steps, a.warmup,
-                                                            not a.no_kernel_timing and not a.graph, a.graph)
-    T = cfg["B"] * cfg["N"]
-    work = kernel_work(cfg, extra)
-    kernels = {}
-    for name, durs in per.items():
-        bound, amount = work[name]
-        avg = sum(durs) / len(durs)
-        per_step = sum(durs) / a.steps
-        peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
-        achieved = amount / avg
-        kernels[name] = {"bound": bound, "avg_us": round(avg * 1e6, 2), "us_per_step": round(per_step * 1e6, 2),
-                         "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
-                         "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4),
-                         "launches_per_step": len(durs) / a.steps}
-        if name in overlapped_groups():
-            kernels[name]["overlapped"] = True   # span includes waiting for compute units
-    roofline = None
-    if kernels and dominant and live:
-        k = kernels[dominant]
-        bound, amount = work[dominant]
-        avg = sum(live) / len(live)                      # from the timed region's events
-        achieved = amount / avg
-        peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
-        roofline = {"kernel": dominant, "bound": bound,
-                    "achieved": round(achieved / (1e9 if bound == "hbm" else 1e12), 2),
-                    "peak": 8000.0 if bound == "hbm" else 2500.0, "unit": k["unit"],
-                    "frac": round(achieved / peak, 4), "avg_us": round(avg * 1e6, 2),
-                    "launches_timed": len(live), "traffic": traffic_of(a.config, dominant)}
+    if a.pmc_table:
+        pmc_table(a.config, a.pmc_table[0], a.pmc_table[1:])
+        return
+    head = measure(a.config, a, True)
     res = {
-        "metric": METRIC, "value": round(T / (ms_step * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "metric": METRIC, "value": head["value"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": head["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: x~N(0,1) seed 1, upstream grad~N(0,1) seed 2, weights nn.Linear init seed 0",
-        "config": {"workload": cfg["workload"], "B": cfg["B"], "N": cfg["N"], "D": cfg["D"], "degree": cfg["K"],
-                   "expand": cfg["E"], "tokens_per_step": T},
-        "fwd_tokens_per_s": round(T / (ms_fwd * 1e-3), 1) if ms_fwd else None,
-        "ms_fwd": round(ms_fwd, 4) if ms_fwd else None, "hip_graph": a.graph,
-        "roofline": roofline, "kernels": kernels,
+        "config": head["config"], "fwd_tokens_per_s": head["fwd_tokens_per_s"], "ms_fwd": head["ms_fwd"],
+        "hip_graph": a.graph, "roofline": head["roofline"], "kernels": head["kernels"],
     }
-    if kernels:
-        agg = [n for n in ("agg_fwd", "agg_bwd", "gate_fwd", "gate_bwd", "gate_heads_fwd", "gate_heads_bwd")
-               if n in kernels]
-        gem = [n for n in kernels if n.startswith("gemm")]
-        t_hbm = sum(kernels[n]["us_per_step"] for n in agg)
-        t_mf = sum(kernels[n]["us_per_step"] for n in gem)
-        b_hbm = sum(work[n][1] for n in agg)
-        f_mf = sum(work[n][1] for n in gem)
-        res["roofline_groups"] = {
-            "hip_streaming_kernels": {"us_per_step": round(t_hbm, 2),
-                                      "frac_hbm": round(b_hbm / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None},
-            "projection_gemms": {"us_per_step": round(t_mf, 2),
-                                 "frac_mfma": round(f_mf / (t_mf * 1e-6) / MFMA_BF16_PEAK, 4) if t_mf else None},
-            "ideal_step_us": round((b_hbm / HBM_PEAK + f_mf / MFMA_BF16_PEAK) * 1e6, 2),
-        }
-    if not a.no_cpu:
-        res["cpu_baseline"] = cpu_run(cfg, a.cpu_seconds)
+    for k in ("roofline_groups", "mall_flushed", "cpu_baseline"):
+        if k in head:
+            res[k] = head[k]
+    subs = [c for c in a.sub_configs.split(",") if c and c != a.config]
+    if subs:
+        res["configs"] = {}
+        for c in subs:
+            r = measure(c, a, False)
+            res["configs"][c] = {k: v for k, v in r.items() if k != "config"}
+            print(f"bench.py: {c} done: {r['ms_per_step']} ms/step", file=sys.stderr, flush=True)
     print(json.dumps(res), flush=True)
 
 
