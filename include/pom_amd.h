@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 8
+#define POM_AMD_ABI_VERSION 9
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -252,6 +252,38 @@ int pom_features_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P
  * take the vector path. */
 int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_t ld_src,
                   void* dst, int64_t ld_dst, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Projection GEMM (matrix cores)
+ * ------------------------------------------------------------------------ */
+
+/* C (M x N, row stride ldc) = A B with bf16 operands and fp32 accumulation,
+ * on `stream`.  Replaces the bf16 nn.Linear products of the projections,
+ * pom/pom.py:187-191 (qc_proj, ag_proj), :205-207 (the fused [h | s]
+ * projection) and :231 (the output projection), and their autograd
+ * backward (data and weight gradients).  Each operand is read in either
+ * row-major layout, so no product needs a transposed copy:
+ *   a_layout POM_GEMM_K_CONTIG : A(m, k) = A[m * lda + k]
+ *            POM_GEMM_MN_CONTIG: A(m, k) = A[k * lda + m]
+ *   b_layout POM_GEMM_K_CONTIG : B(k, n) = B[n * ldb + k]   (an nn.Linear weight, y = x W^T)
+ *            POM_GEMM_MN_CONTIG: B(k, n) = B[k * ldb + n]
+ * out_dtype: POM_DTYPE_BF16 (round to nearest even) or POM_DTYPE_F32.
+ * Requirements (else POM_ERR_UNSUPPORTED): M, N multiples of the chosen
+ * tile, K a multiple of 64, operands and leading dimensions 16-byte
+ * aligned.  tile < 0 and splits <= 0 choose both from the shape
+ * (pom_gemm_plan).  splits > 1 divides K into that many contiguous parts
+ * whose fp32 partials are summed in a fixed order (deterministic), using
+ * pom_gemm_workspace_size() bytes of workspace. */
+typedef enum { POM_GEMM_K_CONTIG = 0, POM_GEMM_MN_CONTIG = 1 } pom_gemm_layout;
+#define POM_GEMM_TILES 6   /* tile ids: 256x256, 256x192, 192x256, 256x128, 128x256, 128x128 (BM x BN) */
+
+/* The tile and split count pom_gemm uses for this shape when asked to
+ * choose; returns POM_ERR_UNSUPPORTED if no tile divides (M, N). */
+int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, int* tile, int* splits);
+size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int splits);
+int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+             const void* B, int64_t ldb, int out_dtype, void* C, int64_t ldc, int tile, int splits,
+             void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,7 +27,7 @@ POM_ERR_DEVICE = 4
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
 MAX_DEGREE = 16
-ABI_VERSION = 8
+ABI_VERSION = 9
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/pom_amd.h declares, with its ctypes signature.
@@ -79,6 +79,10 @@ SIGNATURES = {
     "pom_features_bwd": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _PV, _c_vp, _PV, _PV, _c_vp,
                                   _c_vp, _c_size, _c_vp]),
     "pom_transpose": (_c_int, [_c_int, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp]),
+    "pom_gemm_plan": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int, _c_int, ctypes.POINTER(_c_int), ctypes.POINTER(_c_int)]),
+    "pom_gemm_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "pom_gemm": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp, _c_i64,
+                          _c_int, _c_int, _c_vp, _c_size, _c_vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

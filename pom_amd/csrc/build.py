@@ -8,6 +8,7 @@ from __future__ import annotations
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -15,7 +16,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "transpose.hip", "capi.cpp"]
+SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "transpose.hip", "gemm.hip", "capi.cpp"]
 OUT = os.path.join(PKG, "libpom_amd.so")
 BUILD_DIR = os.path.join(PKG, "_build")
 
@@ -30,13 +31,24 @@ FLAGS = [
 ]
 
 
+def _deps(path: str, seen: set) -> set:
+    """The file and every local header it includes, recursively."""
+    if path in seen or not os.path.exists(path):
+        return seen
+    seen.add(path)
+    with open(path) as f:
+        for line in f:
+            m = re.match(r'\s*#\s*include\s+"([^"]+)"', line)
+            if m:
+                _deps(os.path.normpath(os.path.join(os.path.dirname(path), m.group(1))), seen)
+    return seen
+
+
 def _stale(src: str, obj: str) -> bool:
     if not os.path.exists(obj):
         return True
     t = os.path.getmtime(obj)
-    deps = [os.path.join(HERE, f) for f in os.listdir(HERE) if f.endswith((".h", ".hip", ".cpp"))]
-    deps.append(os.path.join(ROOT, "include", "pom_amd.h"))
-    return any(os.path.getmtime(d) > t for d in deps if d.endswith(".h") or d == os.path.join(HERE, src))
+    return any(os.path.getmtime(d) > t for d in _deps(os.path.join(HERE, src), set()))
 
 
 def _compile(src: str, incremental: bool = False) -> str:

@@ -12,6 +12,7 @@
 #include <string>
 
 #include "../../include/pom_amd.h"
+#include "gemm.h"
 #include "pom_internal.h"
 
 namespace {
@@ -859,6 +860,152 @@ int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_
   if (!aligned(src, eb) || !aligned(dst, eb)) return fail(POM_ERR_INVALID, "src and dst must be element-aligned");
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(pom::transpose_t(eb, src, ld_src, dst, ld_dst, rows, cols, st), "pom_transpose launch");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Projection GEMM
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr int kGemmMaxSplits = 8;
+
+struct GemmCost {
+  double us = 1e30;
+  int tile = -1, splits = 1;
+};
+
+// Modelled time of one (tile, splits) choice: whole rounds of 256 workgroups
+// (one per CU) of the per-workgroup time, plus the fixed-order reduction of
+// the fp32 partials when split.  Smaller tiles run the matrix cores less
+// efficiently (more LDS and L2 traffic per flop).
+double gemm_model_us(int64_t M, int64_t N, int64_t K, int tile, int splits) {
+  int bm, bn;
+  pom::gemm_tile_dims(tile, &bm, &bn);
+  static const double tile_rate[pom::GEMM_TILE_COUNT] = {1.0, 0.97, 0.97, 0.88, 0.88, 0.7};
+  const int64_t units = (M / bm) * (N / bn) * splits;
+  const int64_t rounds = cdiv(units, 256);
+  const double cu_flops = 4.0 * 1024 * 2.1e9 * 0.7 * tile_rate[tile];   // per CU per second
+  const double wg_us = 2.0 * bm * bn * ((double)K / splits) / cu_flops * 1e6
+                       + 1.5 + (double)bm * bn * (splits > 1 ? 4 : 2) / 120e9 * 1e6;
+  double us = rounds * wg_us;
+  if (splits > 1) us += 3.0 + ((double)splits * 4 + 2) * M * N / 4.5e12 * 1e6;
+  return us;
+}
+
+bool gemm_tile_fits(int64_t M, int64_t N, int tile) {
+  int bm, bn;
+  pom::gemm_tile_dims(tile, &bm, &bn);
+  return M % bm == 0 && N % bn == 0;
+}
+
+// POM_AMD_GEMM_FORCE="tile,splits" pins the choice (tile sweeps).
+GemmCost gemm_choose(int64_t M, int64_t N, int64_t K) {
+  GemmCost best;
+  static const char* force = getenv("POM_AMD_GEMM_FORCE");
+  if (force) {
+    int t = -1, sp = 1;
+    if (sscanf(force, "%d,%d", &t, &sp) == 2 && t >= 0 && t < pom::GEMM_TILE_COUNT && sp >= 1 &&
+        sp <= kGemmMaxSplits && gemm_tile_fits(M, N, t) && K / 64 >= sp) {
+      best.tile = t;
+      best.splits = sp;
+      best.us = 0;
+      return best;
+    }
+  }
+  for (int t = 0; t < pom::GEMM_TILE_COUNT; ++t) {
+    if (!gemm_tile_fits(M, N, t)) continue;
+    for (int sp = 1; sp <= kGemmMaxSplits; ++sp) {
+      if (K / 64 < 8 * sp) break;
+      const double us = gemm_model_us(M, N, K, t, sp);
+      if (us < best.us) best = {us, t, sp};
+    }
+  }
+  return best;
+}
+
+size_t gemm_ws_bytes(int64_t M, int64_t N, int splits) {
+  return splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * 4 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, int* tile, int* splits) {
+  (void)a_layout;
+  (void)b_layout;
+  if (M <= 0 || N <= 0 || K <= 0 || K % 64) return fail(POM_ERR_UNSUPPORTED, "gemm: K (%lld) must be a positive multiple of 64", (long long)K);
+  const GemmCost c = gemm_choose(M, N, K);
+  if (c.tile < 0)
+    return fail(POM_ERR_UNSUPPORTED, "gemm: no tile divides M=%lld, N=%lld", (long long)M, (long long)N);
+  if (tile) *tile = c.tile;
+  if (splits) *splits = c.splits;
+  return POM_OK;
+}
+
+size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int splits) {
+  if (tile < 0 || splits <= 0) {
+    int t = -1, sp = 1;
+    if (pom_gemm_plan(M, N, K, 0, 0, &t, &sp) != POM_OK) return 0;
+    if (splits <= 0) splits = sp;
+  }
+  return gemm_ws_bytes(M, N, splits);
+}
+
+int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+             const void* B, int64_t ldb, int out_dtype, void* C, int64_t ldc, int tile, int splits,
+             void* workspace, size_t workspace_bytes, void* stream) {
+  if ((a_layout != POM_GEMM_K_CONTIG && a_layout != POM_GEMM_MN_CONTIG) ||
+      (b_layout != POM_GEMM_K_CONTIG && b_layout != POM_GEMM_MN_CONTIG))
+    return fail(POM_ERR_INVALID, "gemm: layouts must be POM_GEMM_K_CONTIG or POM_GEMM_MN_CONTIG");
+  if (out_dtype != POM_DTYPE_BF16 && out_dtype != POM_DTYPE_F32)
+    return fail(POM_ERR_UNSUPPORTED, "gemm: out_dtype must be bf16 or f32");
+  if (M < 0 || N < 0 || K < 0) return fail(POM_ERR_INVALID, "gemm: negative size");
+  if (M == 0 || N == 0) return POM_OK;
+  if (K == 0 || K % 64) return fail(POM_ERR_UNSUPPORTED, "gemm: K (%lld) must be a positive multiple of 64", (long long)K);
+  if (!A || !B || !C) return fail(POM_ERR_INVALID, "gemm: null operand");
+  const bool amn = a_layout == POM_GEMM_MN_CONTIG, bmn = b_layout == POM_GEMM_MN_CONTIG;
+  if (lda < (amn ? M : K) || ldb < (bmn ? N : K) || ldc < N)
+    return fail(POM_ERR_INVALID, "gemm: leading dimension too small (lda %lld, ldb %lld, ldc %lld)", (long long)lda,
+                (long long)ldb, (long long)ldc);
+  if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16) || lda % 8 || ldb % 8 ||
+      ldc % (out_dtype == POM_DTYPE_F32 ? 4 : 8))
+    return fail(POM_ERR_UNSUPPORTED, "gemm: operands and leading dimensions must be 16-byte aligned");
+  if (tile < 0 || splits <= 0) {
+    const GemmCost c = gemm_choose(M, N, K);
+    if (tile < 0) tile = c.tile;
+    if (splits <= 0) splits = c.splits;
+  }
+  if (tile < 0 || tile >= pom::GEMM_TILE_COUNT || !gemm_tile_fits(M, N, tile))
+    return fail(POM_ERR_UNSUPPORTED, "gemm: tile %d does not divide M=%lld, N=%lld", tile, (long long)M, (long long)N);
+  if (splits > kGemmMaxSplits || splits > K / 64)
+    return fail(POM_ERR_UNSUPPORTED, "gemm: splits (%d) must be <= %d and <= K / 64", splits, kGemmMaxSplits);
+  if (M * N > ((int64_t)1 << 31) || M > INT32_MAX || N > INT32_MAX || K / 64 > INT32_MAX)
+    return fail(POM_ERR_UNSUPPORTED, "gemm: output too large");
+  const size_t need = gemm_ws_bytes(M, N, splits);
+  if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
+    return fail(POM_ERR_WORKSPACE, "gemm: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
+                workspace ? workspace_bytes : (size_t)0);
+  pom::GemmProblem p;
+  p.A = A;
+  p.B = B;
+  p.C = C;
+  p.workspace = workspace;
+  p.lda = lda;
+  p.ldb = ldb;
+  p.ldc = ldc;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.a_mn = amn;
+  p.b_mn = bmn;
+  p.out_f32 = out_dtype == POM_DTYPE_F32;
+  p.tile = tile;
+  p.splits = splits;
+  return hip_status(pom::gemm_bf16(p, static_cast<hipStream_t>(stream)), "pom_gemm launch");
 }
 
 }  // extern "C"

@@ -162,6 +162,78 @@ def _with_copy(call, out_t, src_rows: torch.Tensor, name: str, what: str, B: int
     check(rc, what)
 
 
+# Projection GEMMs on the library's own matrix-core kernel (pom_gemm), which
+# reads every operand in its natural layout.  POM_AMD_HIP_GEMMS names the
+# products that use it: "wgrad" (default: the two weight gradients), "all",
+# "none", or a comma list of gemm_qc_fwd, gemm_ag_fwd, gemm_ag_dgrad,
+# gemm_qc_dgrad, gemm_ag_wgrad, gemm_qc_wgrad.  A product whose shape no tile
+# of the kernel divides, or whose operands are not bf16, stays on hipBLASLt.
+_GEMM_NAMES = ("gemm_qc_fwd", "gemm_ag_fwd", "gemm_ag_dgrad", "gemm_qc_dgrad", "gemm_ag_wgrad", "gemm_qc_wgrad")
+
+
+def _hip_gemm_set() -> frozenset:
+    v = os.environ.get("POM_AMD_HIP_GEMMS", "wgrad").strip()
+    if v == "all":
+        return frozenset(_GEMM_NAMES)
+    if v == "none" or not v:
+        return frozenset()
+    if v == "wgrad":
+        return frozenset(("gemm_ag_wgrad", "gemm_qc_wgrad"))
+    names = frozenset(n.strip() for n in v.split(","))
+    bad = names - set(_GEMM_NAMES)
+    if bad:
+        raise ValueError(f"POM_AMD_HIP_GEMMS: unknown product(s) {sorted(bad)}")
+    return names
+
+
+_HIP_GEMMS = _hip_gemm_set()
+_plan_cache: dict = {}
+
+
+def hip_gemm_fits(name: str, M: int, N: int, K: int, dt: torch.dtype) -> bool:
+    """Whether product `name` of shape (M, N, K) runs on pom_gemm."""
+    if name not in _HIP_GEMMS or dt != torch.bfloat16:
+        return False
+    key = (M, N, K)
+    ok = _plan_cache.get(key)
+    if ok is None:
+        t, sp = ctypes.c_int(), ctypes.c_int()
+        ok = _plan_cache[key] = _lib.load().pom_gemm_plan(M, N, K, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == 0
+    return ok
+
+
+def hip_gemm(a: torch.Tensor, a_mn: bool, b: torch.Tensor, b_mn: bool, out_dtype: torch.dtype = torch.bfloat16,
+             name: str = "gemm") -> torch.Tensor:
+    """C = A B on pom_gemm, bf16 operands, fp32 accumulation.  a is (M, K) with
+    a_mn False or (K, M) with a_mn True; b is (N, K) with b_mn False (an
+    nn.Linear weight: y = x W^T) or (K, N) with b_mn True.  Both 2-D with unit
+    inner stride.  Returns a fresh (M, N) tensor in out_dtype (bf16 or fp32)."""
+    _lib.require_device(a, b)
+    if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
+        raise ValueError("hip_gemm takes bf16 operands")
+    if a.dim() != 2 or b.dim() != 2 or a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("hip_gemm operands must be 2-D with unit inner stride")
+    K, M = (a.shape[0], a.shape[1]) if a_mn else (a.shape[1], a.shape[0])
+    Kb, N = (b.shape[0], b.shape[1]) if b_mn else (b.shape[1], b.shape[0])
+    if Kb != K:
+        raise ValueError(f"hip_gemm: inner dimensions differ ({K} and {Kb})")
+    lib = _lib.load()
+    c = torch.empty(M, N, dtype=out_dtype, device=a.device)
+    wsb = lib.pom_gemm_workspace_size(M, N, K, -1, 0)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=a.device) if wsb else None
+    with _Span(name):
+        rc = lib.pom_gemm(1 if a_mn else 0, 1 if b_mn else 0, M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(),
+                          b.stride(0), dtype_code(c), c.data_ptr(), c.stride(0), -1, 0,
+                          None if ws is None else ws.data_ptr(), wsb, stream_handle(a.device))
+    check(rc, "pom_gemm")
+    return c
+
+
+def _wgrad_dtype(param_dtype: torch.dtype) -> torch.dtype:
+    """Output dtype of a weight gradient: the parameter's, fp32 for anything but bf16."""
+    return torch.bfloat16 if param_dtype == torch.bfloat16 else torch.float32
+
+
 def _weight_t(w: torch.Tensor) -> torch.Tensor:
     """Transposed copy of a projection weight, cached per weight version."""
     return _derived(_wt_cache, w, lambda u: transpose(u.detach(), "transpose_w"))
@@ -641,8 +713,11 @@ class _PoMLayer(torch.autograd.Function):
         dev = x.device
         x2 = x.reshape(T, D)
         nt = training and _NT_GEMMS and dt != torch.float32
-        want_xt = nt and ctx.needs_input_grad[1]
-        want_sht = nt and ctx.needs_input_grad[4]
+        # weight gradients on pom_gemm read x and sh in place; hipBLASLt gets token-contiguous copies
+        hip_wq = training and ctx.needs_input_grad[1] and hip_gemm_fits("gemm_qc_wgrad", W, D, T, dt)
+        hip_wa = training and ctx.needs_input_grad[4] and hip_gemm_fits("gemm_ag_wgrad", D, P, T, dt)
+        want_xt = nt and ctx.needs_input_grad[1] and not hip_wq
+        want_sht = nt and ctx.needs_input_grad[4] and not hip_wa
         cur = torch.cuda.current_stream(dev)
         side = _copy_stream(dev) if (want_xt or want_sht) else None
         xt = sht = None
@@ -682,6 +757,7 @@ class _PoMLayer(torch.autograd.Function):
             if sht is not None and not fused:
                 sht.record_stream(cur)
         ctx.nt = nt
+        ctx.hip_w = (hip_wq, hip_wa)
         ctx.save_for_backward(None if want_xt else x, xt, y, None if want_sht else sh, sht,
                               hagg, c32, b32, wq, wa, mask, count)
         ctx.shape = (B, N, D)
@@ -724,7 +800,13 @@ class _PoMLayer(torch.autograd.Function):
             dsh = torch.mm(g2, wa_k)                                # (T, P)
         dw_ag = None
         over = _OVERLAP_GEMMS and side is not None
-        if need_wa:
+        hip_wq, hip_wa = ctx.hip_w
+        tq, tb, tc, ta, tab = ctx.dtypes
+        if need_wa and hip_wa:
+            if not g2.is_contiguous():
+                g2 = g2.contiguous()
+            dw_ag = hip_gemm(g2, True, sh.view(T, P), True, _wgrad_dtype(ta), "gemm_ag_wgrad")   # (D, P)
+        elif need_wa:
             if gt is not None and over:
                 with torch.cuda.stream(side), _Span("gemm_ag_wgrad"), tuned_gemms():
                     dw_ag = torch.mm(gt, sht.t())                   # (D, P), on the second stream
@@ -774,7 +856,9 @@ class _PoMLayer(torch.autograd.Function):
             wq_k = _weight_t(wq).t() if nt else wq                  # (P+S, D), K-contiguous when nt
             with _Span("gemm_qc_dgrad"), tuned_gemms():
                 dx = torch.mm(dy, wq_k)                             # (T, D)
-        if need_wq and dw_qc is None:
+        if need_wq and dw_qc is None and hip_wq:
+            dw_qc = hip_gemm(dy, True, x.reshape(T, D), True, _wgrad_dtype(tq), "gemm_qc_wgrad")   # (W, D)
+        elif need_wq and dw_qc is None:
             if want_dyt:
                 if not fused:
                     cur.wait_stream(side)
@@ -795,7 +879,6 @@ class _PoMLayer(torch.autograd.Function):
             nf = dh.shape[1]
             w = n_past / (n_past + torch.arange(nf, device=dev, dtype=torch.float32) + 1.0)
             g_carry = (dh * w.view(1, nf, 1)).sum(dim=1, keepdim=True).to(dt)
-        tq, tb, tc, ta, tab = ctx.dtypes
         if dw_qc is not None and dw_qc.shape[0] != P + S:
             dw_qc = dw_qc[:P + S]   # the padding rows' gradient is not a parameter's
         return (None if dx is None else dx.view(B, N, D), None if dw_qc is None else dw_qc.to(tq),

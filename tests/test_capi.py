@@ -34,7 +34,7 @@ def test_header_lists_expected_entry_points():
     for n in ["pom_abi_version", "pom_last_error", "pom_agg_workspace_size", "pom_agg_fwd", "pom_agg_bwd",
               "pom_gate_workspace_size", "pom_gate_fwd", "pom_gate_bwd", "pom_gate_heads_workspace_size",
               "pom_gate_heads_fwd", "pom_gate_heads_bwd", "pom_features_workspace_size", "pom_features_fwd",
-              "pom_features_bwd", "pom_transpose"]:
+              "pom_features_bwd", "pom_transpose", "pom_gemm_plan", "pom_gemm_workspace_size", "pom_gemm"]:
         assert n in names
 
 
@@ -325,3 +325,35 @@ def test_rope_positions_checked_on_host():
         _lib.RopeSpec(_lib.ROPE_2D, [rc, rs, cc, cs], torch.tensor([[4, 0]]))   # row table has 4 rows
     with pytest.raises(IndexError):
         _lib.RopeSpec(_lib.ROPE_2D, [rc, rs, cc, cs], torch.tensor([[0, 6]]))   # column table has 6 rows
+
+
+def test_gemm_plan_and_validation_before_launch(lib):
+    import ctypes
+    from pom_amd import _lib
+    t, sp = ctypes.c_int(-5), ctypes.c_int(-5)
+    # config 2's six projection shapes all have a dividing tile
+    for M, N, K in ((16384, 4608, 1152), (16384, 1152, 2304), (16384, 2304, 1152), (16384, 1152, 4608),
+                    (1152, 2304, 16384), (4608, 1152, 16384)):
+        assert lib.pom_gemm_plan(M, N, K, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_OK
+        assert 0 <= t.value < 6 and 1 <= sp.value <= 8
+        assert (lib.pom_gemm_workspace_size(M, N, K, -1, 0) > 0) == (sp.value > 1)
+    # no tile divides a 64-multiple like 2368 x 1152 (per-head W at config 2); K must be a multiple of 64
+    assert lib.pom_gemm_plan(2368, 1152, 16384, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_ERR_UNSUPPORTED
+    assert lib.pom_gemm_plan(1024, 1024, 100, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_ERR_UNSUPPORTED
+    assert lib.pom_gemm_workspace_size(1024, 1024, 4096, 5, 3) == 3 * 1024 * 1024 * 4
+    assert lib.pom_gemm_workspace_size(1024, 1024, 4096, 5, 1) == 0
+    fake = 1 << 20   # never dereferenced: every call below fails validation before any launch
+    call = lambda al, bl, M, N, K, odt, tile, splits, ws=None, wsb=0, **kw: lib.pom_gemm(
+        al, bl, M, N, K, kw.get("A", fake), kw.get("lda", 1024), kw.get("B", fake), kw.get("ldb", 1024), odt,
+        kw.get("C", fake), kw.get("ldc", 1024), tile, splits, ws, wsb, None)
+    assert call(2, 0, 256, 256, 64, 1, 0, 1) == _lib.POM_ERR_INVALID          # layout
+    assert call(0, 0, 256, 256, 64, 2, 0, 1) == _lib.POM_ERR_UNSUPPORTED      # fp16 output
+    assert call(0, 0, 256, 256, 96, 1, 0, 1) == _lib.POM_ERR_UNSUPPORTED      # K % 64
+    assert call(0, 0, 256, 256, 64, 1, 0, 1, A=0) == _lib.POM_ERR_INVALID     # null operand
+    assert call(0, 0, 256, 256, 2048, 1, 0, 1, lda=1000) == _lib.POM_ERR_INVALID    # lda < K
+    assert call(0, 0, 256, 256, 64, 1, 0, 1, lda=1028) == _lib.POM_ERR_UNSUPPORTED  # 16-byte rows
+    assert call(0, 0, 192, 256, 64, 1, 0, 1) == _lib.POM_ERR_UNSUPPORTED      # tile 0 does not divide M
+    assert call(0, 0, 256, 256, 640, 1, 0, 9) == _lib.POM_ERR_UNSUPPORTED     # too many splits
+    assert call(0, 0, 256, 256, 640, 1, 0, 2) == _lib.POM_ERR_WORKSPACE       # split-K needs workspace
+    assert b"workspace" in lib.pom_last_error()
+    assert call(0, 0, 0, 256, 640, 1, 0, 2) == _lib.POM_OK                    # empty output: nothing to do
