@@ -26,8 +26,8 @@
 //     16-k sub-step, each R rows of 32 bytes plus 32 bytes of padding, rows
 //     and halves permuted within row octets (lds_addr) so that fragment
 //     reads and the stores of either layout are free of bank conflicts, and
-//     all of a lane's fragment reads and stores address off one base
-//     register with immediate offsets;
+//     a lane's fragment reads and stores address off two base registers
+//     with immediate offsets;
 //   * an M/N-contiguous operand is loaded as 8 x 8 blocks (8 k-rows of 8
 //     consecutive m) and transposed in registers (v_perm_b32) before its
 //     LDS store, so both layouts share one LDS layout and one fragment read;
@@ -74,24 +74,22 @@ struct GemmArgs {
 
 // LDS bytes of one operand's sub-array (one 16-k sub-step) and of the operand.
 template <int R>
-constexpr int sub_bytes() { return R * 32 + 64; }
+constexpr int sub_bytes() { return R * 32 + 32; }
 template <int R>
 constexpr int opnd_bytes() { return 4 * sub_bytes<R>(); }
 
-// Row permutation within an octet, by the octet's index mod 4 (0, 1, 4, 5).
-__device__ __forceinline__ int oct_perm(int oct) { return (oct & 1) | ((oct & 2) << 1); }
-
-// Offset of the 16-byte half `h` (k = 16 s + 8 h .. + 7) of row `row` in sub-array s.  The LDS
-// serves a 16-byte read or write 16 lanes at a time from 64 four-byte banks (256 bytes), so 16 lanes
-// must touch 16 distinct 16-byte slots of a 256-byte window.  Rows are 32 bytes, permuted within
-// their octet by oct_perm of the octet index, halves swapped in odd octets, and sub-arrays 64 bytes
-// out of step.  Then 16 consecutive rows of one half (a fragment read), two adjacent rows of all
-// eight halves (a K-contiguous store) and four halves of four consecutive octets' rows (an
-// M/N-contiguous store) all fill the window.
+// Offset of the 16-byte half `h` (k = 16 s + 8 h .. + 7) of row `row` in sub-array s.
+// gfx950's LDS serves a 16-byte read 16 lanes at a time from a 256-byte bank window and a 16-byte
+// write 8 lanes at a time from a 128-byte window (measured with the bank-conflict counter), so the
+// 16 lanes of a read and the 8 lanes of a write must each touch distinct 16-byte slots of their window.
+// Rows are 32 bytes; within a row octet o the rows are permuted by o & 3, the two halves swap when
+// bit 0 of o or bit 2 of o is set, and sub-arrays are 32 bytes out of step.  Then 16 consecutive rows
+// of one half (a fragment read), the 8 halves of one row (a K-contiguous store) and one column of 8
+// consecutive octets (an M/N-contiguous store) all spread over their windows.
 template <int R>
 __device__ __forceinline__ int lds_addr(int s, int row, int h) {
   const int oct = row >> 3;
-  return s * sub_bytes<R>() + ((row ^ oct_perm(oct)) << 5) + ((h ^ (oct & 1)) << 4);
+  return s * sub_bytes<R>() + ((row ^ (oct & 3)) << 5) + ((h ^ (oct & 1) ^ ((oct >> 2) & 1)) << 4);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base, uint32_t bytes) {
@@ -106,67 +104,64 @@ __device__ __forceinline__ u32x4_t buf_load(__amdgpu_buffer_rsrc_t r, uint32_t v
 //   K-contiguous, instruction j of wave w, lane l: row (4 j + w) * 8 + (l >> 3), 16-byte chunk l & 7
 //   (k = 8 (l & 7)); consecutive lanes read consecutive 16-byte pieces of one 128-byte row segment.
 //   M/N-contiguous, block b of the thread (b < R; threads past R repeat b % R and store the same bytes
-//   to the same addresses as its owner): 16 consecutive blocks cover 4 consecutive column octets
-//   (64 contiguous bytes of a k-row) times 4 k-row groups: mo = (b & 3) + 4 (b >> 5),
-//   kg = ((b >> 2) & 3) + 4 ((b >> 4) & 1); the block is k-rows 8 kg .. 8 kg + 7 of columns
-//   8 mo .. 8 mo + 7.
+//   to the same addresses as its owner): columns 8 mo .. 8 mo + 7 with mo = b % (R/8), k-rows
+//   8 kg .. 8 kg + 7 with kg = b / (R/8); 8 consecutive lanes read 128 contiguous bytes of a k-row.
 template <int R, bool MN>
 struct Operand {
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t voff;
   uint32_t sstride;   // K-contiguous: bytes of 32 rows; M/N-contiguous: bytes of one k-row
-  int st0;            // LDS store base (K: row j = 0; M/N: column 0 of the block's permuted octet)
-  int px;             // M/N only: column i of the block is stored at st0 + ((i ^ px) << 5)
+  int st0;            // LDS store base: K: row j at (j odd ? st1 : st0) + 1024 j; M/N: column i at
+  int st1;            //   st0 + ((i ^ st1) << 5)
   __device__ __forceinline__ void init(const uint16_t* base, int64_t ld, uint32_t bytes, int tid, int b) {
     rsrc = make_rsrc(base, bytes);
     if constexpr (MN) {
       b %= R;
-      const int mo = (b & 3) + 4 * (b >> 5), kg = ((b >> 2) & 3) + 4 * ((b >> 4) & 1);
+      const int mo = b % (R / 8), kg = b / (R / 8);
       voff = (uint32_t)(((int64_t)kg * 8 * ld + mo * 8) * 2);
       sstride = (uint32_t)(ld * 2);
-      st0 = lds_addr<R>(kg >> 1, mo * 8, kg & 1) - (oct_perm(mo) << 5);
-      px = oct_perm(mo);
+      st0 = lds_addr<R>(kg >> 1, mo * 8, kg & 1) - ((mo & 3) << 5);
+      st1 = mo & 3;
     } else {
       const int w = tid >> 6, l = tid & 63, c = l & 7, row = w * 8 + (l >> 3);
       voff = (uint32_t)(((int64_t)row * ld + c * 8) * 2);
       sstride = (uint32_t)(ld * 64);
       st0 = lds_addr<R>(c >> 1, row, c & 1);
-      px = 0;
+      st1 = lds_addr<R>(c >> 1, row + 32, c & 1) - 32 * 32;
     }
   }
 };
 
 template <int R, bool MN>
 struct Staged {
-  static constexpr int J = MN ? 8 : R / 32;
+  static constexpr int J = MN ? 8 : R / 32;   // global loads and LDS stores per 64-step
   u32x4_t v[J];
+  // global load j (K-contiguous: rows 32 j ..; M/N-contiguous: k-row j of the block)
+  __device__ __forceinline__ void load_one(const Operand<R, MN>& o, int k0, int j) {
+    const uint32_t soff = MN ? ((uint32_t)k0 + j) * o.sstride : (uint32_t)k0 * 2 + (uint32_t)j * o.sstride;
+    v[j] = buf_load(o.rsrc, o.voff, soff);
+  }
   __device__ __forceinline__ void load(const Operand<R, MN>& o, int k0) {
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t soff = MN ? ((uint32_t)k0 + j) * o.sstride : (uint32_t)k0 * 2 + (uint32_t)j * o.sstride;
-      v[j] = buf_load(o.rsrc, o.voff, soff);
+    for (int j = 0; j < J; ++j) load_one(o, k0, j);
+  }
+  // LDS store j into the operand's region `lds` (M/N-contiguous: column j of the block, which reads
+  // every loaded k-row, so an operand's loads may only follow all of its stores)
+  __device__ __forceinline__ void store_one(char* lds, const Operand<R, MN>& o, int j) const {
+    if constexpr (MN) {
+      // column j: k-pairs (2e, 2e+1) from rows 2e and 2e+1, half j % 2 of dword j / 2
+      const unsigned sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      u32x4_t w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = __builtin_amdgcn_perm(v[2 * e + 1][j >> 1], v[2 * e][j >> 1], sel);
+      *reinterpret_cast<u32x4_t*>(lds + o.st0 + ((j ^ o.st1) << 5)) = w;
+    } else {
+      *reinterpret_cast<u32x4_t*>(lds + ((j & 1) ? o.st1 : o.st0) + j * 32 * 32) = v[j];
     }
   }
-  // store into the operand's LDS region `lds`
-  __device__ __forceinline__ void store(char* lds, const Operand<R, MN>& o) {
-    // The staged data is used from VGPRs: left to itself the register allocator keeps it in AGPRs and
-    // spills accumulators to make room.  (At this point the loads have landed anyway.)
+  __device__ __forceinline__ void store(char* lds, const Operand<R, MN>& o) const {
 #pragma unroll
-    for (int j = 0; j < J; ++j) asm volatile("" : "+v"(v[j]));
-    if constexpr (MN) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        // column i of the block: k-pairs (2e, 2e+1) from rows 2e and 2e+1, half i % 2 of dword i / 2
-        const unsigned sel = (i & 1) ? 0x07060302u : 0x05040100u;
-        u32x4_t w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = __builtin_amdgcn_perm(v[2 * e + 1][i >> 1], v[2 * e][i >> 1], sel);
-        *reinterpret_cast<u32x4_t*>(lds + o.st0 + ((i ^ o.px) << 5)) = w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < J; ++j) *reinterpret_cast<u32x4_t*>(lds + o.st0 + j * 32 * 32) = v[j];
-    }
+    for (int j = 0; j < J; ++j) store_one(lds, o, j);
   }
 };
 
@@ -225,17 +220,20 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
 
   // this lane's fragment rows: A rows wm * WM + 32 i + (lane & 31), B rows wn * WN + 32 j + (lane & 31),
   // half lane >> 5 of each 16-k sub-step
+  // (blocks 2 q and 2 q + 1 differ in the half swap, so even and odd blocks have their own base)
   const int lrow = lane & 31, lhalf = lane >> 5;
-  const int fa = lds_addr<BM>(0, wm * WM + lrow, lhalf);
-  const int fb = A_BYTES + lds_addr<BN>(0, wn * WN + lrow, lhalf);
+  const int fa0 = lds_addr<BM>(0, wm * WM + lrow, lhalf);
+  const int fa1 = lds_addr<BM>(0, wm * WM + 32 + lrow, lhalf) - 32 * 32;
+  const int fb0 = A_BYTES + lds_addr<BN>(0, wn * WN + lrow, lhalf);
+  const int fb1 = A_BYTES + lds_addr<BN>(0, wn * WN + 32 + lrow, lhalf) - 32 * 32;
 
   auto read_frags = [&](const char* st, int s, bf16x8_t (&af)[MB], bf16x8_t (&bfr)[NB]) {
 #pragma unroll
     for (int i = 0; i < MB; ++i)
-      af[i] = *reinterpret_cast<const bf16x8_t*>(st + fa + s * sub_bytes<BM>() + i * 32 * 32);
+      af[i] = *reinterpret_cast<const bf16x8_t*>(st + ((i & 1) ? fa1 : fa0) + s * sub_bytes<BM>() + i * 32 * 32);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
-      bfr[j] = *reinterpret_cast<const bf16x8_t*>(st + fb + s * sub_bytes<BN>() + j * 32 * 32);
+      bfr[j] = *reinterpret_cast<const bf16x8_t*>(st + ((j & 1) ? fb1 : fb0) + s * sub_bytes<BN>() + j * 32 * 32);
   };
   auto mfmas = [&](const bf16x8_t (&af)[MB], const bf16x8_t (&bfr)[NB]) {
 #pragma unroll
@@ -244,24 +242,53 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
       for (int j = 0; j < NB; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[j], af[i], acc[i][j], 0, 0, 0);
   };
-  // One 64-step on stage `cur` in four sections, one per 16-k sub-step, fenced from each other so the
-  // compiler keeps this order: the staged tile of register set (sa, sb) is written into stage `nxt`
-  // in sections 0-1 (A, then B), the set is refilled with the tile at k0 in sections 2-3, and each
-  // section reads the next sub-step's fragments before its own MFMAs.
+  // One 64-step on stage `cur`: the staged tile of register set (sa, sb) is written into stage `nxt`,
+  // the set is refilled with the tile at k0, and the four 16-k sub-steps' MFMAs run on fragments read
+  // one sub-step ahead.  The memory instructions are spread one or two at a time between the MFMAs,
+  // in a fixed order (a scheduling fence after each MFMA slot): issued in bursts, the global loads and
+  // LDS stores back up the address and LDS queues and block the wave from issuing MFMAs (measured:
+  // about a third of a step).  The stores take the first two sub-steps and the loads the last two,
+  // so every load refills registers whose store has issued.
+  constexpr int NMF = MB * NB, NRD = MB + NB;
+  constexpr int JA = Staged<BM, A_MN>::J, JB = Staged<BN, B_MN>::J, NWR = JA + JB;
   auto step64 = [&](const char* cur, char* nxt, Staged<BM, A_MN>& sa, Staged<BN, B_MN>& sb, int k0) {
     bf16x8_t af[2][MB], bfr[2][NB];
     read_frags(cur, 0, af[0], bfr[0]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (q == 0) sa.store(nxt, oa);
-      if (q == 1) sb.store(nxt + A_BYTES, ob);
-      if (q == 2) sa.load(oa, k0);
-      if (q == 3) sb.load(ob, k0);
-      if (q < 3) read_frags(cur, q + 1, af[(q + 1) & 1], bfr[(q + 1) & 1]);
-      mfmas(af[q & 1], bfr[q & 1]);
+#pragma unroll
+      for (int m = 0; m < NMF; ++m) {
+        const int i = m / NB, j = m % NB;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[q & 1][j], af[q & 1][i], acc[i][j], 0, 0, 0);
+        if (q < 3) {   // next sub-step's fragments r in [lo, hi)
+          const int lo = (m * NRD + NMF - 1) / NMF, hi = ((m + 1) * NRD + NMF - 1) / NMF;
+#pragma unroll
+          for (int r = lo; r < hi; ++r) {
+            if (r < MB)
+              af[(q + 1) & 1][r] = *reinterpret_cast<const bf16x8_t*>(
+                  cur + ((r & 1) ? fa1 : fa0) + (q + 1) * sub_bytes<BM>() + r * 32 * 32);
+            else
+              bfr[(q + 1) & 1][r - MB] = *reinterpret_cast<const bf16x8_t*>(
+                  cur + (((r - MB) & 1) ? fb1 : fb0) + (q + 1) * sub_bytes<BN>() + (r - MB) * 32 * 32);
+          }
+        }
+        // stores (sub-steps 0-1) or loads (sub-steps 2-3) w in [lo, hi) of NWR
+        const int g = (q & 1) * NMF + m;
+        const int lo = (g * NWR + 2 * NMF - 1) / (2 * NMF), hi = ((g + 1) * NWR + 2 * NMF - 1) / (2 * NMF);
+#pragma unroll
+        for (int w = lo; w < hi; ++w) {
+          if (q < 2) {
+            if (w < JA) sa.store_one(nxt, oa, w);
+            else sb.store_one(nxt + A_BYTES, ob, w - JA);
+          } else {
+            if (w < JA) sa.load_one(oa, k0, w);
+            else sb.load_one(ob, k0, w - JA);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
   };
 
