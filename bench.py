@@ -571,6 +571,12 @@ def _is_gate_bwd(name: str) -> bool:
     return any(k in name for k in ("gate_bwd_kernel", "heads_bwd_rows", "heads_bwd_tile", "heads_bwd_token_kernel"))
 
 
+def _is_gemm(name: str) -> bool:
+    """A projection GEMM dispatch: a hipBLASLt kernel or this library's pom_gemm kernel (whose
+    split-K reduction, when present, is the next dispatch and counts with it)."""
+    return "Cijk" in name or "gemm_bf16_kernel" in name
+
+
 def _gemm_dispatches(db: str):
     """Dispatch id and library kernel name of each projection GEMM of the last
     complete fwd+bwd step, from the dispatch order: qc_fwd precedes
@@ -585,9 +591,15 @@ def _gemm_dispatches(db: str):
     order = ["gemm_qc_fwd", "gemm_ag_fwd", "gemm_ag_dgrad", "gemm_ag_wgrad", "gemm_qc_dgrad", "gemm_qc_wgrad"]
     gb = max(i for i, (_, n) in enumerate(seq) if _is_gate_bwd(n))
     af = max(i for i, (_, n) in enumerate(seq[:gb]) if "agg_fwd_chunk" in n)
-    pre = [d for d in seq[:af] if "Cijk" in d[1]]
-    gemms = [pre[-1]] + [d for d in seq[af:] if "Cijk" in d[1]][:5]
-    return {g: (d, n[:160]) for g, (d, n) in zip(order, gemms)}
+    pre = [i for i, d in enumerate(seq[:af]) if _is_gemm(d[1])]
+    idx = [pre[-1]] + [af + i for i, d in enumerate(seq[af:]) if _is_gemm(d[1])][:5]
+    out = {}
+    for g, i in zip(order, idx):
+        ds = [seq[i][0]]
+        if i + 1 < len(seq) and "gemm_splitk_reduce" in seq[i + 1][1]:
+            ds.append(seq[i + 1][0])
+        out[g] = (ds, seq[i][1][:160])
+    return out
 
 
 def _pmc_dispatch(db: str, counter: str):
@@ -629,8 +641,8 @@ def pmc_summary(cfg_name, dbs):
     # projection GEMMs: the dispatches of the last complete step, by order
     gd = _gemm_dispatches(dbs[0])
     fd, wd = _pmc_dispatch(dbs[0], "FETCH_SIZE"), _pmc_dispatch(dbs[1], "WRITE_SIZE")
-    for g, (d, _) in gd.items():
-        groups[g] = fd.get(d, 0.0) * 1024.0 * f_scale + wd.get(d, 0.0) * 1024.0 * w_scale
+    for g, (ds, _) in gd.items():
+        groups[g] = sum(fd.get(d, 0.0) * 1024.0 * f_scale + wd.get(d, 0.0) * 1024.0 * w_scale for d in ds)
     out["gemm_kernels"] = {g: n for g, (_, n) in gd.items()}
     out["groups"] = groups
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
@@ -662,8 +674,8 @@ def pmc_table(cfg_name, db, counters):
         if row:
             out["groups"][g] = row
     gd = _gemm_dispatches(db)
-    for g, (d, kname) in gd.items():
-        out["groups"][g] = {c: _pmc_dispatch(db, c).get(d) for c in counters}
+    for g, (ds, kname) in gd.items():
+        out["groups"][g] = {c: _pmc_dispatch(db, c).get(ds[0]) for c in counters}
         out["groups"][g]["kernel"] = kname
     path = os.path.join(ROOT, "profiles", f"pmc_{cfg_name}_{counters[0]}.json")
     with open(path, "w") as f:
@@ -673,8 +685,8 @@ def pmc_table(cfg_name, db, counters):
 
 def trace_summary(trace_dir):
     """Table of a kernel-trace run: calls, average us, share of GPU time, kernel
-    (library GEMMs labelled with their projection from the dispatch order of
-    the last fwd+bwd step)."""
+    (GEMMs labelled with their projection from the dispatch order of the
+    fwd+bwd steps)."""
     import csv
     stats = list(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_stats.csv"))))
     trace = sorted(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_trace.csv"))),
@@ -690,18 +702,22 @@ def trace_summary(trace_dir):
         end = afs[k + 1] if k + 1 < len(afs) else len(seq)
         if not any(_is_gate_bwd(n) for n in seq[af:end]):
             continue   # a forward-only pass
-        pre = [i for i in range(af) if "Cijk" in seq[i]]
-        idx = [pre[-1]] + [i for i in range(af, end) if "Cijk" in seq[i]][:5]
+        pre = [i for i in range(af) if _is_gemm(seq[i])]
+        idx = [pre[-1]] + [i for i in range(af, end) if _is_gemm(seq[i])][:5]
         for g, i in zip(order, idx):
-            per[g].append(dur[i])
+            red = i + 1 < len(seq) and "gemm_splitk_reduce" in seq[i + 1]
+            per[g].append(dur[i] + (dur[i + 1] if red else 0.0))
             label.setdefault(seq[i], set()).add(g)
+            if red:
+                label.setdefault(seq[i + 1], set()).add(g)
     print("# columns: calls, avg_us, pct_of_gpu_time, kernel (library GEMM names truncated)")
     for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"])):
         name = r["Name"]
         tag = f"   [{', '.join(sorted(label[name]))}]" if name in label else ""
         print(f"{int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} {float(r['Percentage']):6.2f}  "
               f"{name[:100]}{tag}")
-    print("# projection GEMMs of the fwd+bwd steps, labelled by dispatch order: group, calls, avg_us")
+    print("# projection GEMMs of the fwd+bwd steps, labelled by dispatch order (a split-K reduction counted with "
+          "its GEMM): group, calls, avg_us")
     for g in order:
         if per[g]:
             print(f"#   {g:14s} {len(per[g]):4d} {sum(per[g]) / len(per[g]):10.2f}")

@@ -277,8 +277,11 @@ int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_
 typedef enum { POM_GEMM_K_CONTIG = 0, POM_GEMM_MN_CONTIG = 1 } pom_gemm_layout;
 #define POM_GEMM_TILES 6   /* tile ids: 256x256, 256x192, 192x256, 256x128, 128x256, 128x128 (BM x BN) */
 
-/* The tile and split count pom_gemm uses for this shape when asked to
- * choose; returns POM_ERR_UNSUPPORTED if no tile divides (M, N). */
+/* The tile and split count pom_gemm uses for this shape and these layouts
+ * when asked to choose (a measured table for the baseline configurations'
+ * weight gradients, else a cost model); returns POM_ERR_UNSUPPORTED if no
+ * tile divides (M, N).  pom_gemm_workspace_size with tile < 0 reports the
+ * largest need of the four layouts' plans. */
 int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, int* tile, int* splits);
 size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int splits);
 int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,

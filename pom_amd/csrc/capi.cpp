@@ -901,8 +901,26 @@ bool gemm_tile_fits(int64_t M, int64_t N, int tile) {
   return M % bm == 0 && N % bn == 0;
 }
 
-// POM_AMD_GEMM_FORCE="tile,splits" pins the choice (tile sweeps).
-GemmCost gemm_choose(int64_t M, int64_t N, int64_t K) {
+// Measured best (tile, splits) for the weight-gradient products of the baseline configurations
+// (M/N-contiguous operands; MI355X, isolated runs over every tile and 1-8 splits).
+struct GemmTuned {
+  int64_t M, N, K;
+  int a_layout, b_layout, tile, splits;
+};
+const GemmTuned kGemmTuned[] = {
+    {1152, 2304, 16384, 1, 1, 2, 4},  // config 2: dW_ag = g^T sh
+    {4608, 1152, 16384, 1, 1, 1, 2},  // config 2: dW_qc = dY^T x
+    {1024, 2048, 65536, 1, 1, 0, 8},  // config 3
+    {4096, 1024, 65536, 1, 1, 0, 4},
+    {1024, 4096, 65536, 1, 1, 0, 4},  // config 4
+    {8192, 1024, 65536, 1, 1, 0, 4},
+    {1536, 3072, 32768, 1, 1, 0, 7},  // config 5
+    {6144, 1536, 32768, 1, 1, 0, 3},
+};
+
+// POM_AMD_GEMM_FORCE="tile,splits" pins the choice (tile sweeps); then the measured table; then the
+// cost model.
+GemmCost gemm_choose(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout) {
   GemmCost best;
   static const char* force = getenv("POM_AMD_GEMM_FORCE");
   if (force) {
@@ -911,6 +929,14 @@ GemmCost gemm_choose(int64_t M, int64_t N, int64_t K) {
         sp <= kGemmMaxSplits && gemm_tile_fits(M, N, t) && K / 64 >= sp) {
       best.tile = t;
       best.splits = sp;
+      best.us = 0;
+      return best;
+    }
+  }
+  for (const GemmTuned& e : kGemmTuned) {
+    if (e.M == M && e.N == N && e.K == K && e.a_layout == a_layout && e.b_layout == b_layout) {
+      best.tile = e.tile;
+      best.splits = e.splits;
       best.us = 0;
       return best;
     }
@@ -935,10 +961,8 @@ size_t gemm_ws_bytes(int64_t M, int64_t N, int splits) {
 extern "C" {
 
 int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, int* tile, int* splits) {
-  (void)a_layout;
-  (void)b_layout;
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return fail(POM_ERR_UNSUPPORTED, "gemm: K (%lld) must be a positive multiple of 64", (long long)K);
-  const GemmCost c = gemm_choose(M, N, K);
+  const GemmCost c = gemm_choose(M, N, K, a_layout, b_layout);
   if (c.tile < 0)
     return fail(POM_ERR_UNSUPPORTED, "gemm: no tile divides M=%lld, N=%lld", (long long)M, (long long)N);
   if (tile) *tile = c.tile;
@@ -947,10 +971,16 @@ int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, i
 }
 
 size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int splits) {
-  if (tile < 0 || splits <= 0) {
-    int t = -1, sp = 1;
-    if (pom_gemm_plan(M, N, K, 0, 0, &t, &sp) != POM_OK) return 0;
-    if (splits <= 0) splits = sp;
+  if (tile < 0 || splits <= 0) {   // the largest need over both layouts' plans
+    size_t need = 0;
+    for (int al = 0; al < 2; ++al)
+      for (int bl = 0; bl < 2; ++bl) {
+        int t = -1, sp = 1;
+        if (pom_gemm_plan(M, N, K, al, bl, &t, &sp) != POM_OK) return 0;
+        const size_t b = gemm_ws_bytes(M, N, splits <= 0 ? sp : splits);
+        need = b > need ? b : need;
+      }
+    return need;
   }
   return gemm_ws_bytes(M, N, splits);
 }
@@ -975,7 +1005,7 @@ int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const 
       ldc % (out_dtype == POM_DTYPE_F32 ? 4 : 8))
     return fail(POM_ERR_UNSUPPORTED, "gemm: operands and leading dimensions must be 16-byte aligned");
   if (tile < 0 || splits <= 0) {
-    const GemmCost c = gemm_choose(M, N, K);
+    const GemmCost c = gemm_choose(M, N, K, a_layout, b_layout);
     if (tile < 0) tile = c.tile;
     if (splits <= 0) splits = c.splits;
   }
