@@ -77,6 +77,10 @@ _COPY_STREAM = os.environ.get("POM_AMD_COPY_STREAM", "1") != "0"
 # chain) also run on the second stream, concurrently with the gating /
 # aggregation backward and the data-gradient GEMMs.
 _OVERLAP_GEMMS = os.environ.get("POM_AMD_OVERLAP_GEMMS", "0") == "1"
+# POM_AMD_SIDE_WGRAD=1: dW_ag on pom_gemm runs on the second stream, beside
+# ag_dgrad and the gate / aggregation backward (its units fill fewer CUs
+# than the chip has).
+_SIDE_WGRAD = os.environ.get("POM_AMD_SIDE_WGRAD", "0") == "1"
 
 
 def _copy_stream(device: torch.device) -> torch.cuda.Stream:
@@ -802,10 +806,17 @@ class _PoMLayer(torch.autograd.Function):
         over = _OVERLAP_GEMMS and side is not None
         hip_wq, hip_wa = ctx.hip_w
         tq, tb, tc, ta, tab = ctx.dtypes
+        side_wa = None
         if need_wa and hip_wa:
             if not g2.is_contiguous():
                 g2 = g2.contiguous()
-            dw_ag = hip_gemm(g2, True, sh.view(T, P), True, _wgrad_dtype(ta), "gemm_ag_wgrad")   # (D, P)
+            if _SIDE_WGRAD and _COPY_STREAM:
+                side_wa = _copy_stream(dev)
+                side_wa.wait_stream(cur)
+                with torch.cuda.stream(side_wa):
+                    dw_ag = hip_gemm(g2, True, sh.view(T, P), True, _wgrad_dtype(ta), "gemm_ag_wgrad")   # (D, P)
+            else:
+                dw_ag = hip_gemm(g2, True, sh.view(T, P), True, _wgrad_dtype(ta), "gemm_ag_wgrad")   # (D, P)
         elif need_wa:
             if gt is not None and over:
                 with torch.cuda.stream(side), _Span("gemm_ag_wgrad"), tuned_gemms():
@@ -868,6 +879,9 @@ class _PoMLayer(torch.autograd.Function):
             else:
                 with _Span("gemm_qc_wgrad"), tuned_gemms():
                     dw_qc = torch.mm(dy.t(), x.reshape(T, D))       # (P+S, D)
+        if side_wa is not None:
+            cur.wait_stream(side_wa)   # join before g2 or sh can be freed
+            dw_ag.record_stream(cur)
         if side is not None:
             cur.wait_stream(side)   # join before g2 or dy can be freed
             if over:
