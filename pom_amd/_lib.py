@@ -223,15 +223,17 @@ def invalidate_derived() -> None:
         c.clear()
 
 
-def derived(cache: dict, t: "torch.Tensor", make):
+def derived(cache: dict, t: "torch.Tensor", make, always: bool = False):
     """``make(t)``: a copy derived from parameter ``t``.  With the cache on
     (set_derived_cache), the copy is kept while that same tensor object is
     alive and unchanged by identity, storage pointer and version counter;
     keyed by object identity, so a freed tensor's address or id reused by a
     new tensor can never hit a stale copy.  Under stream capture the copy is
     always rebuilt, so a captured graph recomputes it on every replay (a replay
-    runs no Python and would otherwise keep the capture-time copy)."""
-    if not _cache_on or (t.is_cuda and torch.cuda.is_current_stream_capturing()):
+    runs no Python and would otherwise keep the capture-time copy).
+    ``always``: cache even with the cache off (tensors that are not trained,
+    e.g. RoPE tables, whose version only moves when they are rewritten)."""
+    if not (_cache_on or always) or (t.is_cuda and torch.cuda.is_current_stream_capturing()):
         return make(t)
     if not any(c is cache for c in _derived_caches):
         _derived_caches.append(cache)
@@ -255,10 +257,11 @@ _table_cache: dict = {}
 
 def _f32_table(t: torch.Tensor) -> torch.Tensor:
     """fp32 contiguous view or cached copy of a RoPE table (a module buffer,
-    bf16 in a bf16 model): converted once per table version, not per call."""
+    bf16 in a bf16 model): converted once per table version, not per call,
+    whether or not the parameter cache is on (tables are not trained)."""
     if t.dtype == torch.float32 and t.is_contiguous():
         return t
-    return derived(_table_cache, t, lambda u: u.detach().float().contiguous())
+    return derived(_table_cache, t, lambda u: u.detach().float().contiguous(), always=True)
 
 
 # POM_AMD_CHECK_POSITIONS=1: also range-check RoPE positions that live on the

@@ -115,6 +115,42 @@ __device__ __forceinline__ void walk_rows(const RowWalk& W, Load&& load, Work&& 
   }
 }
 
+// walk_rows with a prefetch stage for loads whose addresses depend on other
+// loads (RoPE: a row's table entries on its position).  pre(pb, base) loads
+// the addresses of the step at `base` (rows clamped into the chunk) one step
+// ahead, so load(bf, pb, base, clamp) issues the dependent loads at once,
+// next to the row loads.  Vector memory operations complete in issue order,
+// so a load is waited for together with everything issued before it: the
+// prefetch is issued with the step's loads, before the step's stores, and
+// the next step waits for it without waiting for those.  load() must end
+// with a fence for memory operations (mem_fence_compiler) so that no pass
+// moves the prefetch after the stores.  The chunk must hold at least one row.
+template <typename Buf, typename Pre, typename PreLoad, typename Load, typename Work>
+__device__ __forceinline__ void walk_rows_pre(const RowWalk& W, PreLoad&& pre, Load&& load, Work&& work) {
+  const int64_t nfull = W.full_steps();
+  Pre pc;
+  pre(pc, 0);
+  for (int64_t it = 0; it < nfull; ++it) {
+    Pre pn;
+    Buf bf;
+    pre(pn, (it + 1) * W.step);
+    load(bf, pc, it * W.step, false);
+    work(bf, it * W.step, std::false_type{});
+    pc = pn;
+  }
+  if (W.has_tail()) {
+    Buf bf;
+    load(bf, pc, nfull * W.step, true);
+    work(bf, nfull * W.step, std::true_type{});
+  }
+}
+
+// A compiler fence for memory operations (no instruction is emitted): no
+// load or store is moved across it by any pass, where a sched_barrier holds
+// only in the machine scheduler.  Used after a step's loads so that each is
+// issued there rather than sunk to its first use and waited for on the spot.
+__device__ __forceinline__ void mem_fence_compiler() { asm volatile("" ::: "memory"); }
+
 // Channel-major copy of one workgroup step, staged through LDS.  The step
 // covers tokens [tok0, tok0 + S) of batch row b, S = kWaves * rpw * U, for
 // the lpr * NS channel slots of the slab; each lane holds U consecutive tokens
@@ -700,6 +736,245 @@ agg_bwd_chunk_w3(const AggParams p) {
   agg_bwd_body<T, CPT, KM, MODE, TR>(p);
 }
 
+// ---------------------------------------------------------------------------
+// RoPE backward with one lane per half of a rotation pair (HalfMap).
+// grad_x of a channel at token n is act'(x) p'(h) times its upstream weight
+// rotated back to the token: w cos + sign w_partner sin, from the cos / sin
+// table row of n's position (pom/pom_rope.py:258-296 differentiated).  The
+// upstream weights are constant over the chunk, so nothing but that table row
+// couples the two halves: a lane holds the coefficients and sums of its own
+// CPT channels only, half the state of a pair lane.
+// The table row of a position serves every batch row (positions are per
+// token), so a workgroup walks NB batch rows at once: a lane loads the table
+// entries of U tokens and the x of those tokens in NB batch rows, NB x U = 4
+// rows in flight for U table lookups.  At NB = 4 the lookups cost 2 bytes per
+// element instead of 8 (at C5's shape: 105-116 us against 142-148 for
+// NB = 1).  The NB batch rows' upstream weights are read from LDS at each row
+// (in registers they would hold the kernel under three waves per SIMD).
+// NB divides B (the host picks it so), so every row of the walk exists and
+// the stores need no branch.  grad_coeff partials are per (batch group,
+// chunk): the NB rows of a token are added in batch order, the tokens in walk
+// order.  The step's loads are issued before its arithmetic (walk_rows_pre).
+// ---------------------------------------------------------------------------
+template <int NB>
+struct RopeHalfShape {
+  static constexpr int U = NB >= 4 ? 1 : (NB == 2 ? 2 : 4);   // token rows per step
+};
+
+// o = p[0 .. V) from LDS in 16-byte (or narrower) reads; p aligned to them.
+template <int V>
+__device__ __forceinline__ void lds_load_f32(const float* p, float (&o)[V]) {
+  if constexpr (V % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < V; i += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(p + i);
+      o[i] = a.x; o[i + 1] = a.y; o[i + 2] = a.z; o[i + 3] = a.w;
+    }
+  } else if constexpr (V == 2) {
+    const float2 a = *reinterpret_cast<const float2*>(p);
+    o[0] = a.x; o[1] = a.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = p[i];
+  }
+}
+
+template <typename T, int CPT, int KM, int MODE, int NB>
+__device__ __forceinline__ void agg_bwd_rope_half_body(const AggParams& p) {
+  using Map = HalfMap<CPT, MODE>;
+  constexpr bool MASKED = mode_masked(MODE);
+  static_assert(!MASKED || NB == 1, "masked rows are walked one batch row at a time");
+  constexpr int U = RopeHalfShape<NB>::U;
+  __shared__ float red[kWaves][kMaxLpr * CPT];
+
+  const LaneGeom G(p.g.lpr_log2);
+  const int64_t slab = blockIdx.x, chunk = blockIdx.y, bg = blockIdx.z;
+  const int64_t b0 = bg * NB;
+  int64_t f, rbeg, rend;
+  chunk_rows(p.g, chunk, p.N, f, rbeg, rend);
+  const int64_t vcol = slab * G.lpr + G.lcol;
+  const bool active = vcol < p.g.nvec;
+  Map map;
+  map.init(active ? vcol : 0, p.P);
+
+  // d[i][j] = (j+1) c[i][j]; wsh[k][0 / 1] = own and (signed) partner upstream
+  // weights of batch row b0 + k, one slot per channel of the slab
+  float d[CPT][KM], g[CPT][KM];
+  __shared__ __attribute__((aligned(16))) float wsh[NB][2][kMaxLpr * CPT];
+  {
+    float flat[CPT * KM];
+    param_gather<CPT * KM>(p.coeff, [&](int q) {
+      const int j = q % KM;
+      return map.chan(q / KM) * p.K + (j < p.K ? j : p.K - 1);
+    }, flat);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i)
+#pragma unroll
+      for (int j = 0; j < KM; ++j) {
+        d[i][j] = (active && j < p.K) ? flat[i * KM + j] * (float)(j + 1) : 0.0f;
+        g[i][j] = 0.0f;
+      }
+  }
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const int64_t bk = b0 + k;
+    float cntv = 1.0f;
+    if constexpr (MASKED) cntv = p.count_in[bk];
+    const float* wsrc = (!MASKED && p.wf) ? p.wf + (bk * p.g.F + f) * p.P : p.go + bk * p.P;
+    float raw[2 * CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      raw[i] = wsrc[map.c1 + i];
+      raw[CPT + i] = wsrc[map.cp + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * CPT; ++i) {
+      float wi;
+      if constexpr (MASKED) wi = cntv != 0.0f ? raw[i] / cntv : 0.0f;
+      else if (p.wf) wi = raw[i];
+      else wi = (raw[i] / ((float)p.n_past + 1.0f)) / (float)p.g.L;
+      raw[i] = active ? wi : 0.0f;
+    }
+    if (G.wave == 0 && G.lrow == 0) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        wsh[k][0][G.lcol * CPT + i] = raw[i];
+        wsh[k][1][G.lcol * CPT + i] = map.sign * raw[CPT + i];
+      }
+    }
+  }
+  __syncthreads();
+
+  auto xrow = [&](int k) { return reinterpret_cast<const T*>(p.x) + (b0 + k) * p.sxb; };
+  if constexpr (MASKED) {
+    // rows before the first and after the last valid row: zero gradient, x not read
+    T* gxb = reinterpret_cast<T*>(p.gx) + b0 * p.sgb;
+    int64_t first, last;
+    float unused;
+    mask_extent(p, b0, rbeg, rend, first, last, unused);
+    if (last < first) first = last = rend;
+    else ++last;
+    if (active) {
+      float z[CPT];
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) z[i] = 0.0f;
+      for (int64_t n = rbeg + G.wave * G.rpw + G.lrow; n < first; n += G.rs)
+        VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
+      for (int64_t n = last + G.wave * G.rpw + G.lrow; n < rend; n += G.rs)
+        VecIO<T, CPT>::store(gxb + n * p.sgn + map.c1, z);
+    }
+    rbeg = first;
+    rend = last;
+  }
+  const RowWalk W(rbeg, rend, G.wave * G.rpw + G.lrow, G.rs, U);
+
+  struct Pos {
+    int tp[U];   // table positions, loaded one step ahead
+  };
+  struct Buf {
+    Pack<T, CPT> v[U][NB];
+    float mv[MASKED ? U : 1];
+    float cs[U][CPT], sn[U][CPT];
+  };
+  auto pre = [&](Pos& pb, int64_t base) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) pb.tp[u] = rope_pos(p.rope, map.table, W.row(base, u, true));
+  };
+  auto load = [&](Buf& bf, const Pos& pb, int64_t base, bool clamp) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_table_at<CPT>(p.rope, map.table, pb.tp[u], map.tcol, bf.cs[u], bf.sn[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t rr = W.row(base, u, clamp);
+#pragma unroll
+      for (int k = 0; k < NB; ++k) bf.v[u][k].load_stream(xrow(k) + rr * p.sxn + map.c1);
+      if constexpr (MASKED) bf.mv[u] = p.mask[b0 * p.msb + rr * p.msn];
+    }
+    mem_fence_compiler();   // every load of the step issued before its arithmetic
+  };
+  auto step = [&](const Buf& bf, int64_t base, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool in = !TAIL || W.valid(base, u);
+      const int64_t n = W.row(base, u, TAIL);
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        bool keep = in;
+        float mw = 1.0f;
+        if constexpr (MASKED) {
+          keep = keep && bf.mv[u] != 0.0f;
+          mw = bf.mv[u];
+        }
+        float gv[CPT], wok[CPT], wpk[CPT];
+        lds_load_f32<CPT>(&wsh[k][0][G.lcol * CPT], wok);
+        lds_load_f32<CPT>(&wsh[k][1][G.lcol * CPT], wpk);
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const float we = (wok[i] * bf.cs[u][i] + wpk[i] * bf.sn[u][i]) * mw;
+          const float x = bf.v[u][k].get(i);
+          const float l = leaky(x), h = clamp_act(l);
+          gv[i] = weighted_act_grad(x, l, h, we, 0.01f * we) * poly_d<KM>(h, d[i]);
+          if constexpr (MASKED) gv[i] = keep ? gv[i] : 0.0f;   // padded token: zero gradient
+          pow_acc<KM>((MASKED || TAIL) ? (keep ? h : 0.0f) : h, we, g[i]);
+        }
+        if (in)
+          VecIO<T, CPT>::store(reinterpret_cast<T*>(p.gx) + (b0 + k) * p.sgb + n * p.sgn + map.c1, gv);
+      }
+    }
+  };
+  if (active && W.nrows > 0) walk_rows_pre<Buf, Pos>(W, pre, load, step);
+
+  // grad_coeff partial of the chunk, one degree at a time.
+  const int nslot = G.lpr * CPT;
+  for (int j = 0; j < p.K; ++j) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      float v = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < KM; ++jj) v = (jj == j) ? g[i][jj] : v;
+      v = xor_sum_rows(v, G.lb);
+      if (G.lrow == 0) red[G.wave][G.lcol * CPT + i] = v;
+    }
+    __syncthreads();
+    for (int s = G.tid; s < nslot; s += kThreads) {
+      const int l = s / CPT, i = s - l * CPT;
+      const int64_t vc = slab * G.lpr + l;
+      if (vc >= p.g.nvec) continue;
+      float v = 0.0f;
+#pragma unroll
+      for (int w2 = 0; w2 < kWaves; ++w2) v += red[w2][s];
+      p.part[((bg * p.g.nch + chunk) * p.K + j) * p.P + vc * CPT + i] = v;
+    }
+    __syncthreads();
+  }
+}
+
+// Three waves per SIMD where the state fits 168 VGPRs without spilling
+// (degree <= 3 at NB = 4, <= 2 at NB = 2, 1 at NB = 1, unmasked); the rest run
+// uncapped, as capped they spill inside the row loop.
+template <int CPT, int KM, int MODE, int NB>
+constexpr bool kRopeHalfW3 = !mode_masked(MODE) && (NB >= 4 ? KM <= 3 : (NB == 2 ? KM <= 2 : KM <= 1));
+
+template <typename T, int CPT, int KM, int MODE, int NB>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
+agg_bwd_rope_half_w3(const AggParams p) {
+  agg_bwd_rope_half_body<T, CPT, KM, MODE, NB>(p);
+}
+
+template <typename T, int CPT, int KM, int MODE, int NB>
+__global__ void __launch_bounds__(kThreads) agg_bwd_rope_half(const AggParams p) {
+  agg_bwd_rope_half_body<T, CPT, KM, MODE, NB>(p);
+}
+
+template <typename T, int CPT, int KM, int MODE, int NB>
+void launch_rope_half(const AggParams& p, dim3 grid, hipStream_t st) {
+  if constexpr (kRopeHalfW3<CPT, KM, MODE, NB>)
+    hipLaunchKernelGGL((agg_bwd_rope_half_w3<T, CPT, KM, MODE, NB>), grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((agg_bwd_rope_half<T, CPT, KM, MODE, NB>), grid, dim3(kThreads), 0, st, p);
+}
+
 // grad_coeff[c, j] = sum over the rows (batch row, chunk) of the partials.
 // A workgroup owns 64 outputs.  From 64 rows on, each of its four waves sums
 // a quarter of the rows (sixteen loads in flight, in row order) and the
@@ -771,22 +1046,55 @@ hipError_t agg_fwd_mode(const AggParams& p, hipStream_t st) {
 template <typename T, int CPT, int KM, bool TR>
 hipError_t agg_bwd_tr(const AggParams& p, hipStream_t st) {
   const dim3 grid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)p.B), block(kThreads);
+  if (p.g.half) {   // RoPE modes without the channel-major copy
+    if constexpr (TR) {
+      return hipErrorInvalidValue;
+    } else {
+      auto launch = [&](auto nb_tag) -> hipError_t {
+        constexpr int NB = decltype(nb_tag)::value;
+        const dim3 hgrid((unsigned)p.g.nslabs, (unsigned)p.g.nch, (unsigned)(p.B / NB));
+        switch (p.mode) {
+          case MODE_ROPE1D:
+            launch_rope_half<T, CPT, KM, MODE_ROPE1D, NB>(p, hgrid, st);
+            break;
+          case MODE_ROPE2D:
+            launch_rope_half<T, CPT, KM, MODE_ROPE2D, NB>(p, hgrid, st);
+            break;
+          case MODE_ROPE1D_MASKED:
+            if constexpr (NB != 1) return hipErrorInvalidValue;
+            else launch_rope_half<T, CPT, KM, MODE_ROPE1D_MASKED, 1>(p, hgrid, st);
+            break;
+          case MODE_ROPE2D_MASKED:
+            if constexpr (NB != 1) return hipErrorInvalidValue;
+            else launch_rope_half<T, CPT, KM, MODE_ROPE2D_MASKED, 1>(p, hgrid, st);
+            break;
+          default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+      };
+      if constexpr (CPT >= 4) {
+        if (p.g.nb == 4) return launch(std::integral_constant<int, 4>{});
+        if (p.g.nb == 2) return launch(std::integral_constant<int, 2>{});
+      }
+      if (p.g.nb == 1) return launch(std::integral_constant<int, 1>{});
+      return hipErrorInvalidValue;
+    }
+  }
   switch (p.mode) {
     case MODE_PLAIN:
       if constexpr (KM <= 2) hipLaunchKernelGGL((agg_bwd_chunk_w3<T, CPT, KM, MODE_PLAIN, TR>), grid, block, 0, st, p);
       else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_PLAIN, TR>), grid, block, 0, st, p);
       break;
     case MODE_MASKED: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_MASKED, TR>), grid, block, 0, st, p); break;
-    case MODE_ROPE1D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D, TR>), grid, block, 0, st, p); break;
-    case MODE_ROPE2D: hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D, TR>), grid, block, 0, st, p); break;
-    // masked RoPE: no channel-major copy (the C ABI rejects the request)
-    case MODE_ROPE1D_MASKED:
-      if constexpr (TR) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D_MASKED, false>), grid, block, 0, st, p);
+    // RoPE with pair lanes: only with the channel-major copy (without it the
+    // half-pair kernel above runs; masked RoPE has no copy, the C ABI rejects it)
+    case MODE_ROPE1D:
+      if constexpr (!TR) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE1D, true>), grid, block, 0, st, p);
       break;
-    case MODE_ROPE2D_MASKED:
-      if constexpr (TR) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D_MASKED, false>), grid, block, 0, st, p);
+    case MODE_ROPE2D:
+      if constexpr (!TR) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((agg_bwd_chunk<T, CPT, KM, MODE_ROPE2D, true>), grid, block, 0, st, p);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -870,7 +1178,7 @@ hipError_t agg_bwd_t(const AggParams& p, hipStream_t st) {
     if (hipError_t e = hipGetLastError()) return e;
   }
   if (hipError_t e = agg_bwd_chunks<T>(p, st)) return e;
-  return launch_coeff_grad_finalize(p.part, p.B * p.g.nch, p.P, p.K, p.gc, st);
+  return launch_coeff_grad_finalize(p.part, p.B / p.g.nb * p.g.nch, p.P, p.K, p.gc, st);
 }
 
 }  // namespace pom

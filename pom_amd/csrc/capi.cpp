@@ -682,6 +682,19 @@ int pom_agg_bwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t P, int
     return hip_status(by_dtype(dtype, [&](auto t) { return pom::scan_bwd_t<decltype(t)>(s, st); }),
                       "pom_agg_bwd (token-causal) launch");
   }
+  if (is_rope(p.mode) && !grad_x_t) {
+    // one lane per half of a rotation pair (the units become channels), and
+    // with 16- or 8-byte lanes up to four batch rows per workgroup sharing
+    // each table lookup
+    p.g.half = 1;
+    p.g.nb = (mask || p.g.cpt < 4) ? 1 : (B % 4 == 0 ? 4 : (B % 2 == 0 ? 2 : 1));
+    p.g.nvec *= 2;
+    choose_slabs(p.g);
+    choose_chunks(p.g, B / p.g.nb, tune().agg_target_wg);
+    if (p.g.nslabs > 0x7fffffffLL || p.g.nch > 65535)
+      return fail(POM_ERR_UNSUPPORTED, "grid too large (slabs %lld, chunks %lld)", (long long)p.g.nslabs,
+                  (long long)p.g.nch);
+  }
   p.n_past = n_past;
   p.go = grad_out;
   p.count_in = count;

@@ -72,6 +72,36 @@ struct LaneMap {
   }
 };
 
+// RoPE mapping with one lane per half of a rotation pair (the aggregation
+// backward's): a lane owns CPT consecutive channels [c1, c1 + CPT), all first
+// or all second halves of CPT consecutive pairs.  cp is the partner half's
+// first channel and sign the sign of the partner's term in the transposed
+// rotation: a first half's upstream weight is w cos + w_partner sin, a
+// second half's w cos - w_partner sin.
+//   1-D: channels [0, P/2) are first halves (partner c + P/2), table column c.
+//   2-D: q = P/4; [0, q) and [q, 2q) are the first and second halves on the
+//        row tables, [2q, 3q) and [3q, 4q) on the column tables.
+// A lane never straddles two blocks: CPT divides P/2 (1-D) or P/4 (2-D).
+template <int CPT, int MODE>
+struct HalfMap {
+  static constexpr int LAY = mode_layout(MODE);
+  int64_t c1 = 0, cp = 0, tcol = 0;
+  int table = 0;
+  float sign = 1.0f;
+
+  __device__ __forceinline__ void init(int64_t vcol, int64_t P) {
+    c1 = vcol * CPT;
+    const int64_t q = LAY == MODE_ROPE1D ? P / 2 : P / 4;
+    const int64_t blk = c1 / q;
+    const bool second = (blk & 1) != 0;
+    table = LAY == MODE_ROPE1D ? 0 : (int)(blk >> 1);
+    tcol = c1 - blk * q;
+    cp = second ? c1 - q : c1 + q;
+    sign = second ? -1.0f : 1.0f;
+  }
+  __device__ __forceinline__ int64_t chan(int i) const { return c1 + i; }
+};
+
 // Slot s of the partial buffers -> channel (same mapping as LaneMap).
 template <int CPT, int MODE>
 __device__ __forceinline__ int64_t slot_chan(int64_t s, int64_t P) {

@@ -56,6 +56,8 @@ struct Geom {
   int64_t RC = 0;       // rows per chunk
   int64_t cpf = 1;      // chunks per frame = ceil(L / RC)
   int64_t nch = 1;      // chunks per batch row = F * cpf
+  int half = 0;         // RoPE: one lane per half of a rotation pair (units = channels)
+  int nb = 1;           // batch rows per workgroup (divides B; > 1 only with `half`)
 };
 
 // A parameter vector (coefficients, gate bias) or its gradient, in the

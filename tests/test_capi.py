@@ -305,6 +305,24 @@ def test_derived_copies_rebuilt_by_default_and_cache_opt_in(monkeypatch):
         _lib.set_derived_cache(False)
 
 
+def test_rope_table_copies_cached_with_the_cache_off(monkeypatch):
+    """A bf16 RoPE table (a module buffer in a bf16 model) is converted to fp32
+    once per table version, also with the parameter cache off; an in-place
+    write (version bump) is seen; an fp32 contiguous table is used as is."""
+    from pom_amd import _lib
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    assert not _lib.derived_cache_enabled()
+    t = torch.linspace(-1, 1, 64).reshape(4, 16).to(torch.bfloat16)
+    a = _lib._f32_table(t)
+    assert a.dtype == torch.float32 and torch.equal(a, t.float())
+    assert _lib._f32_table(t) is a
+    t.mul_(2)
+    b = _lib._f32_table(t)
+    assert b is not a and torch.equal(b, t.float())
+    f = torch.zeros(4, 16)
+    assert _lib._f32_table(f) is f
+
+
 def test_rope_positions_checked_on_host():
     """Host positions must lie in [-rows, rows) (the range torch's indexing of
     the tables accepts, pom/pom_rope.py:173-174); negatives are passed through

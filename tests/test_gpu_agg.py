@@ -269,6 +269,22 @@ def test_rope2d_masked(device, B, H, W, D, K, dtype):
     run_case(device, B, H * W, D, K, dtype, "masked", keep=0.5, rope=_rope2d(D, H, W), strided=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B", [1, 2, 3, 4, 6, 8])
+def test_rope_backward_batch_groups(device, B, dtype):
+    """The RoPE backward walks NB batch rows per workgroup (4, 2 or 1: the
+    largest dividing B), one lane per half of a rotation pair, each table
+    lookup shared by the NB rows.  Every NB, with groups of one and of several,
+    1-D and 2-D, a degree that runs at three waves per SIMD (2) and one that
+    does not (8), token counts whose chunks end in a partial step (200 and
+    12 x 20), and frames (the per-frame weights of the block-causal mean)."""
+    for K in (2, 8):
+        run_case(device, B, 200, 64, K, dtype, "mean", rope=_rope1d(64, 200, random_pos=True),
+                 strided=dtype != torch.float32)
+        run_case(device, B, 12 * 20, 64, K, dtype, "mean", rope=_rope2d(64, 12, 20), strided=True)
+    run_case(device, B, 256, 64, 3, dtype, "block", frame_len=64, rope=_rope1d(64, 256))
+
+
 def test_rope_masked_invariants(device):
     """Masked RoPE: an all-ones mask gives the RoPE mean, an all-zero row gives
     0, padded tokens (even huge ones) never change the output or get a
