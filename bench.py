@@ -123,6 +123,13 @@ def make_inputs(cfg):
     return x, go, extra
 
 
+def _native_sequence() -> bool:
+    """Whether the layer's steps run the C++ launch sequence (pom_layer_fwd /
+    _bwd) rather than the Python one."""
+    from pom_amd import ops
+    return ops.native_layer_calls[0] > 0
+
+
 def make_module(cfg):
     import torch
     import pom_amd
@@ -263,10 +270,18 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
         return (t1 - t0) / steps * 1e3, None, {}, extra, (None, None)
 
     # instrumented pass: K steps with HIP events around every launch group on
-    # its launch stream -> per-kernel durations and the dominant kernel
+    # its launch stream -> per-kernel durations and the dominant kernel.  The
+    # layer's C++ launch sequence (pom_layer_fwd / _bwd) is one call per
+    # direction with no Python between its launches, so the instrumented
+    # passes run the Python sequence, which launches the same kernels with the
+    # same GEMM solutions on the same operands (bit-identical results,
+    # tests/test_gpu_layer_native.py); the timed region runs the default one.
+    native = ops._NATIVE_LAYER
     per = {}
     dominant = None
+    live = None
     if kernel_timing:
+        ops._NATIVE_LAYER = False
         ops.kernel_timer = []
         for _ in range(steps):
             step()
@@ -277,10 +292,18 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
         # include the wait for free compute units, so they are reported but
         # never taken as the dominant kernel
         dominant = max((k for k in per if k not in overlapped_groups()), key=lambda k: sum(per[k]))
-        # the timed region records events around the dominant kernel only
-        # (events around every launch would add ~5 % to the step)
+        # a timed pass with events around the dominant kernel only (events
+        # around every launch would add ~5 % to the step)
         ops.kernel_timer = []
         ops.kernel_timer_only = {dominant}
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        live = [s.elapsed_time(e) * 1e-3 for _, s, e in ops.kernel_timer]
+        ops.kernel_timer = None
+        ops.kernel_timer_only = None
+        ops._NATIVE_LAYER = native
 
     # timed region: K fwd+bwd steps
     torch.cuda.synchronize()
@@ -290,11 +313,6 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms_step = (t1 - t0) / steps * 1e3
-    live = None
-    if kernel_timing:
-        live = [s.elapsed_time(e) * 1e-3 for _, s, e in ops.kernel_timer]
-        ops.kernel_timer = None
-        ops.kernel_timer_only = None
 
     # forward-only throughput (no autograd graph)
     with torch.no_grad():
@@ -342,6 +360,10 @@ def flushed_layer(cfg, steps, warmup):
         ops.invalidate_derived()
         fwd(m, xd).backward(god)
 
+    # per-kernel spans need the Python launch sequence (same kernels, same
+    # solutions as the C++ one)
+    native = ops._NATIVE_LAYER
+    ops._NATIVE_LAYER = False
     for _ in range(warmup):
         step()
     spans = []
@@ -354,6 +376,7 @@ def flushed_layer(cfg, steps, warmup):
         e1.record()
         spans.append((e0, e1))
     torch.cuda.synchronize()
+    ops._NATIVE_LAYER = native
     per = {}
     for name, a, b in ops.kernel_timer:
         per.setdefault(name, []).append(a.elapsed_time(b) * 1e-3)
@@ -788,7 +811,7 @@ def measure(name, a, headline):
     if kernels and dominant and live:
         k = kernels[dominant]
         bound, amount, copy = work[dominant]
-        avg = sum(live) / len(live)                      # from the timed region's events
+        avg = sum(live) / len(live)                      # events of the timed dominant-kernel pass
         achieved = amount / avg
         peak = HBM_PEAK if bound == "hbm" else MFMA_BF16_PEAK
         roofline = {"kernel": dominant, "bound": bound,
@@ -849,6 +872,7 @@ def main():
         "data": "synthetic: x~N(0,1) seed 1, upstream grad~N(0,1) seed 2, weights nn.Linear init seed 0",
         "config": head["config"], "fwd_tokens_per_s": head["fwd_tokens_per_s"], "ms_fwd": head["ms_fwd"],
         "hip_graph": a.graph, "roofline": head["roofline"], "kernels": head["kernels"],
+        "launch_sequence": "c++" if _native_sequence() else "python",
     }
     for k in ("roofline_groups", "mall_flushed", "cpu_baseline"):
         if k in head:

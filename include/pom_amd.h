@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define POM_AMD_ABI_VERSION 9
+#define POM_AMD_ABI_VERSION 10
 #define POM_MAX_DEGREE 16
 
 typedef enum { POM_DTYPE_F32 = 0, POM_DTYPE_BF16 = 1, POM_DTYPE_F16 = 2 } pom_dtype;
@@ -287,6 +287,110 @@ size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int sp
 int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
              const void* B, int64_t ldb, int out_dtype, void* C, int64_t ldc, int tile, int splits,
              void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Library GEMMs of the fused layer (rocBLAS / hipBLASLt, by solution index)
+ * ------------------------------------------------------------------------ */
+
+/* C (n x m, row stride ldc) = A B^T for bf16 A (m x k, row stride lda) and
+ * B (n x k, row stride ldb), fp32 accumulation -- BLAS's column-major
+ * C = A^T B with transa = T, transb = N -- on `stream`, with the library
+ * solution registered for exactly this (m, n, k, lda, ldb, ldc).  This is the
+ * form of every projection product of the fused layer when its operands are
+ * contiguous along the reduction (pom/pom.py:187-191, :205-207, :231 and
+ * their backward).  No counterpart in the reference, which calls its GEMMs
+ * through torch: these entry points let the layer's launch sequence run in
+ * C++ with the kernels torch's offline-tuned selection table names
+ * (pom_amd/tuned/gemm_gfx950.csv), registered by the caller.  Unregistered
+ * shapes are refused (POM_ERR_UNSUPPORTED); there is no heuristic fallback.
+ * hipBLASLt solutions may need workspace (POM_ERR_WORKSPACE when short). */
+typedef enum { POM_BLAS_ROCBLAS = 1, POM_BLAS_HIPBLASLT = 2 } pom_blas_lib;
+
+int pom_blas_set_solution(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc, int lib,
+                          int index);
+/* 1 when a solution is registered for the shape, else 0. */
+int pom_blas_has_solution(int64_t m, int64_t n, int64_t k, int64_t lda, int64_t ldb, int64_t ldc);
+int pom_blas_gemm(int64_t m, int64_t n, int64_t k, const void* A, int64_t lda, const void* B, int64_t ldb, void* C,
+                  int64_t ldc, void* workspace, size_t workspace_bytes, void* stream);
+/* The file of the loaded rocBLAS (POM_BLAS_ROCBLAS) or hipBLASLt library
+ * these calls go to: solution indices are those of that build. */
+const char* pom_blas_library(int lib);
+
+/* ------------------------------------------------------------------------
+ * The fused layer, one call per direction (pom/pom.py:216-231 with
+ * _get_h_s :204-207 and pom() :125-135; RoPE pom/pom_rope.py:476-526):
+ *   forward : Y = x Wq^T (T x W) -> hagg = aggregate(Y[:, :P]) ->
+ *             sh = gate(Y[:, P:P+S], hagg) -> out = sh Wa^T (+ b_ag)
+ *   backward: dsh = g Wa; dW_ag = g^T sh; db_ag = sum_t g; dY[:, P:P+S],
+ *             dL/dhagg from the gate; dY[:, :P], dcoeff from the
+ *             aggregation; dx = dY Wq; dW_qc = dY^T x
+ * for bf16 activations and weights, T = B * N tokens.  No counterpart in
+ * the reference (whose layer is a chain of torch calls): it replaces the
+ * Python operator's launch sequence so that an eager step spends no host
+ * time between launches.  Every projection runs through pom_blas_gemm and
+ * each weight gradient on pom_gemm when a tile divides it, else through
+ * pom_blas_gemm on the token-contiguous copies xt, sht, gt, dyt (which must
+ * then be given); a library product whose shape has no registered solution
+ * makes the call return POM_ERR_UNSUPPORTED before anything is launched.  The aggregation (mask, frames,
+ * carry, RoPE) and gating (full width or per head) options are those of
+ * pom_agg_* and pom_gate[_heads]_*.  All launches go to `stream`; the
+ * workspace holds pom_layer_workspace_size() bytes.
+ * ------------------------------------------------------------------------ */
+typedef struct pom_layer_args {
+  int64_t B, N, D, P;
+  int64_t S;              /* gate width: P, or heads when heads > 1 */
+  int64_t W;              /* row width of Y and dY, >= P + S (padding columns zero in Wq) */
+  int64_t heads;          /* > 1: per-head gate */
+  int K;                  /* polynomial degree */
+  int param_dtype;        /* se_bias, coeff and their gradients */
+  int bias_ag_dtype;      /* b_ag */
+  int64_t frame_len, n_past;
+  const void* wq;         /* (W, D) bf16 */
+  const void* wq_t;       /* (D, W) bf16, backward with dx */
+  const void* wa;         /* (D, P) bf16 */
+  const void* wa_t;       /* (P, D) bf16, backward */
+  const void* se_bias;    /* (S,) or NULL */
+  const void* coeff;      /* (P, K) */
+  const void* b_ag;       /* (D,) or NULL */
+  const float* mask;      /* (B, N) fp32 weights or NULL */
+  int64_t mask_stride_b, mask_stride_n;
+  const void* carry;      /* (B, P) bf16 running mean or NULL */
+  const pom_rope* rope_h; /* aggregation side, or NULL */
+  const pom_rope* rope_s; /* gate side, or NULL */
+  /* activations (forward outputs, backward inputs) */
+  const void* x;          /* (T, D) */
+  void* xt;               /* (D, T) or NULL */
+  void* y;                /* (T, W) */
+  void* hagg;             /* (B, N / frame_len, P) */
+  float* count;           /* (B,) when masked */
+  void* sh;               /* (T, P) */
+  void* sht;              /* (P, T) or NULL */
+  void* out;              /* (T, D), forward */
+  /* backward */
+  const void* g;          /* (T, D) upstream gradient */
+  void* gt;               /* (D, T) scratch or NULL */
+  void* dsh;              /* (T, P) scratch */
+  void* dy;               /* (T, W) scratch */
+  void* dyt;              /* (W, T) scratch or NULL */
+  void* dx;               /* (T, D) or NULL: not wanted */
+  void* dwq;              /* (W, D) in dwq_dtype, or NULL */
+  int dwq_dtype;
+  void* dwa;              /* (D, P) in dwa_dtype, or NULL */
+  int dwa_dtype;
+  void* dse_bias;         /* (S,) in param_dtype, or NULL */
+  void* dcoeff;           /* (P, K) in param_dtype */
+  float* db_ag;           /* (D,) fp32, or NULL */
+  float* dh;              /* (B, N / frame_len, P) fp32: dL/dhagg */
+  const float* grad_hagg; /* (B, N / frame_len, P) fp32 added to dh, or NULL */
+  void* workspace;
+  size_t workspace_bytes;
+} pom_layer_args;
+
+/* sizeof(pom_layer_args), for bindings to check their copy of the layout */
+size_t pom_layer_args_size(void);
+size_t pom_layer_workspace_size(const pom_layer_args* args, int backward);
+int pom_layer_fwd(const pom_layer_args* args, void* stream);
+int pom_layer_bwd(const pom_layer_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,7 +27,7 @@ POM_ERR_DEVICE = 4
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 ROPE_NONE, ROPE_1D, ROPE_2D = 0, 1, 2
 MAX_DEGREE = 16
-ABI_VERSION = 9
+ABI_VERSION = 10
 NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Every symbol include/pom_amd.h declares, with its ctypes signature.
@@ -49,6 +49,22 @@ class PomRope(ctypes.Structure):
 
 class PomTView(ctypes.Structure):
     _fields_ = [("data", _c_vp), ("stride_c", _c_i64), ("stride_b", _c_i64)]
+
+
+class PomLayerArgs(ctypes.Structure):
+    """pom_layer_args (include/pom_amd.h), field for field; load() checks its size."""
+    _fields_ = [("B", _c_i64), ("N", _c_i64), ("D", _c_i64), ("P", _c_i64), ("S", _c_i64), ("W", _c_i64),
+                ("heads", _c_i64), ("K", _c_int), ("param_dtype", _c_int), ("bias_ag_dtype", _c_int),
+                ("frame_len", _c_i64), ("n_past", _c_i64),
+                ("wq", _c_vp), ("wq_t", _c_vp), ("wa", _c_vp), ("wa_t", _c_vp), ("se_bias", _c_vp), ("coeff", _c_vp),
+                ("b_ag", _c_vp), ("mask", _c_vp), ("mask_stride_b", _c_i64), ("mask_stride_n", _c_i64),
+                ("carry", _c_vp), ("rope_h", ctypes.POINTER(PomRope)), ("rope_s", ctypes.POINTER(PomRope)),
+                ("x", _c_vp), ("xt", _c_vp), ("y", _c_vp), ("hagg", _c_vp), ("count", _c_vp), ("sh", _c_vp),
+                ("sht", _c_vp), ("out", _c_vp),
+                ("g", _c_vp), ("gt", _c_vp), ("dsh", _c_vp), ("dy", _c_vp), ("dyt", _c_vp), ("dx", _c_vp),
+                ("dwq", _c_vp), ("dwq_dtype", _c_int), ("dwa", _c_vp), ("dwa_dtype", _c_int),
+                ("dse_bias", _c_vp), ("dcoeff", _c_vp), ("db_ag", _c_vp), ("dh", _c_vp), ("grad_hagg", _c_vp),
+                ("workspace", _c_vp), ("workspace_bytes", _c_size)]
 
 
 _PV = ctypes.POINTER(PomView)
@@ -83,7 +99,17 @@ SIGNATURES = {
     "pom_gemm_workspace_size": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "pom_gemm": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_int, _c_vp, _c_i64,
                           _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "pom_blas_set_solution": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "pom_blas_has_solution": (_c_int, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
+    "pom_blas_gemm": (_c_int, [_c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_size,
+                               _c_vp]),
+    "pom_blas_library": (ctypes.c_char_p, [_c_int]),
+    "pom_layer_args_size": (_c_size, []),
+    "pom_layer_workspace_size": (_c_size, [ctypes.POINTER(PomLayerArgs), _c_int]),
+    "pom_layer_fwd": (_c_int, [ctypes.POINTER(PomLayerArgs), _c_vp]),
+    "pom_layer_bwd": (_c_int, [ctypes.POINTER(PomLayerArgs), _c_vp]),
 }
+BLAS_ROCBLAS, BLAS_HIPBLASLT = 1, 2
 
 _lib: Optional[ctypes.CDLL] = None
 _lib_lock = threading.Lock()
@@ -108,6 +134,8 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         if lib.pom_abi_version() != ABI_VERSION:
             raise RuntimeError("pom_amd: ABI version mismatch; rebuild libpom_amd.so")
+        if lib.pom_layer_args_size() != ctypes.sizeof(PomLayerArgs):
+            raise RuntimeError("pom_amd: pom_layer_args layout differs from PomLayerArgs; rebuild libpom_amd.so")
         _lib = lib
     return _lib
 

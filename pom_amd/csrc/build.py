@@ -16,7 +16,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "transpose.hip", "gemm.hip", "capi.cpp"]
+SOURCES = ["kernels_bf16.hip", "kernels_f16.hip", "kernels_f32.hip", "transpose.hip", "gemm.hip", "capi.cpp",
+           "layer.cpp"]
 OUT = os.path.join(PKG, "libpom_amd.so")
 BUILD_DIR = os.path.join(PKG, "_build")
 
@@ -70,7 +71,11 @@ def build(jobs: int = 4, verbose: bool = True, incremental: bool = False) -> str
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, incremental), SOURCES))
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    # rocBLAS / hipBLASLt by SONAME: in a process that imported torch first these
+    # resolve to torch's loaded copies (pom_blas_library reports which)
+    rocm_lib = os.path.join(os.environ.get("ROCM_PATH", "/opt/rocm"), "lib")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+           f"-L{rocm_lib}", "-lrocblas", "-lhipblaslt"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

@@ -581,6 +581,14 @@ int scratch_for_current_device(void** out) {
 
 }  // namespace
 
+namespace pom {
+// The calling thread's pom_last_error() message, for the other C ABI files.
+int set_error(int code, const char* msg) {
+  g_err = msg;
+  return code;
+}
+}  // namespace pom
+
 extern "C" {
 
 int pom_abi_version(void) { return POM_AMD_ABI_VERSION; }

@@ -282,4 +282,7 @@ template <typename T> hipError_t heads_bwd_t(const HeadsParams& p, hipStream_t s
 hipError_t transpose_t(int elem_bytes, const void* src, int64_t lds, void* dst, int64_t ldd, int64_t R, int64_t C,
                        hipStream_t st);
 
+// Sets the calling thread's pom_last_error() message and returns `code`.
+int set_error(int code, const char* msg);
+
 }  // namespace pom

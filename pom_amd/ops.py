@@ -26,6 +26,7 @@ import torch
 
 from . import _lib
 from ._lib import RopeSpec, check, derived as _derived, dtype_code, ptr, rope_ptr, view3, workspace, stream_handle
+from . import gemm_select
 from .gemm_select import tuned_gemms
 
 
@@ -684,6 +685,151 @@ def gate_heads_hip(ys: torch.Tensor, bias: Optional[torch.Tensor], hagg: torch.T
 # Fused PoM layer: qc_proj GEMM -> aggregation -> gating -> ag_proj GEMM
 # ---------------------------------------------------------------------------
 
+# The layer's launch sequence in C++ (pom_layer_fwd / pom_layer_bwd: one C
+# call per direction, library GEMMs with the tuned table's solutions) for bf16
+# with the default GEMM options; POM_AMD_NATIVE_LAYER=0 keeps the Python one.
+# A shape the C path does not cover (no registered GEMM solution) falls back
+# to the Python sequence before anything is launched.
+_NATIVE_LAYER = os.environ.get("POM_AMD_NATIVE_LAYER", "1") != "0"
+native_layer_calls = [0, 0]   # forward, backward calls that took the C sequence
+
+
+def _native_layer_usable(dt: torch.dtype, c32: torch.Tensor, b32: torch.Tensor) -> bool:
+    return (_NATIVE_LAYER and dt == torch.bfloat16 and _NT_GEMMS and _NT_COPIES == "fused" and not _OVERLAP_GEMMS
+            and not _SIDE_WGRAD and _HIP_GEMMS == frozenset(("gemm_ag_wgrad", "gemm_qc_wgrad"))
+            and c32.dtype == b32.dtype and gemm_select.native_ready())
+
+
+def _pom_gemm_fits(M: int, N: int, T: int) -> bool:
+    """A weight gradient (M x N over T tokens, token-major operands) that pom_gemm takes."""
+    t, s = ctypes.c_int(-1), ctypes.c_int(0)
+    return _lib.load().pom_gemm_plan(M, N, T, 1, 1, ctypes.byref(t), ctypes.byref(s)) == 0
+
+
+def _layer_args(B, N, D, P, S, W, heads, k, frame_len, n_past, c32, b32, keep) -> "_lib.PomLayerArgs":
+    a = _lib.PomLayerArgs()
+    a.B, a.N, a.D, a.P, a.S, a.W, a.heads, a.K = B, N, D, P, S, W, heads, k
+    a.param_dtype = dtype_code(c32)
+    a.frame_len, a.n_past = frame_len, n_past
+    a.coeff, a.se_bias = c32.data_ptr(), b32.data_ptr()
+    keep.extend((c32, b32))
+    return a
+
+
+def _set_rope(a, rope_h, rope_s, keep) -> None:
+    for name, spec in (("rope_h", rope_h), ("rope_s", rope_s)):
+        if spec is not None:
+            r = spec.struct()
+            keep.append(r)
+            setattr(a, name, ctypes.pointer(r))
+
+
+def _native_layer_forward(x2, wq, wa, b_ag, b32, c32, k, frame_len, mask, carry, n_past, rope_h, rope_s, heads,
+                          B, N, D, P, S, W, want_xt, want_sht):
+    """One pom_layer_fwd call; None when the C path does not cover the shapes
+    (nothing launched)."""
+    lib = _lib.load()
+    dev, dt, T = x2.device, x2.dtype, B * N
+    keep = []
+    a = _layer_args(B, N, D, P, S, W, heads, k, frame_len, n_past, c32, b32, keep)
+    y = torch.empty(T, W, dtype=dt, device=dev)
+    hagg = torch.empty(B, N // frame_len, P, dtype=dt, device=dev)
+    count = torch.empty(B, dtype=torch.float32, device=dev) if mask is not None else None
+    sh = torch.empty(T, P, dtype=dt, device=dev)
+    out = torch.empty(T, D, dtype=dt, device=dev)
+    xt = torch.empty(D, T, dtype=dt, device=dev) if want_xt else None
+    sht = torch.empty(P, T, dtype=dt, device=dev) if want_sht else None
+    a.wq, a.wa, a.x, a.y, a.hagg, a.sh, a.out = (wq.data_ptr(), wa.data_ptr(), x2.data_ptr(), y.data_ptr(),
+                                                 hagg.data_ptr(), sh.data_ptr(), out.data_ptr())
+    a.xt, a.sht, a.count = ptr(xt), ptr(sht), ptr(count)
+    if b_ag is not None:
+        a.b_ag, a.bias_ag_dtype = b_ag.data_ptr(), dtype_code(b_ag)
+        keep.append(b_ag)
+    if mask is not None:
+        a.mask, a.mask_stride_b, a.mask_stride_n = mask.data_ptr(), mask.stride(0), mask.stride(1)
+    if carry is not None:
+        carry = carry.reshape(B, P).to(dt).contiguous()
+        a.carry = carry.data_ptr()
+        keep.append(carry)
+    _set_rope(a, rope_h, rope_s, keep)
+    ws = workspace(dev, lib.pom_layer_workspace_size(ctypes.byref(a), 0))
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    with _Span("layer_fwd"):
+        rc = lib.pom_layer_fwd(ctypes.byref(a), stream_handle(dev))
+    if rc == _lib.POM_ERR_UNSUPPORTED:
+        return None
+    check(rc, "pom_layer_fwd")
+    native_layer_calls[0] += 1
+    return y, hagg, count, sh, out, xt, sht
+
+
+def _native_layer_backward(ctx, grad_out, grad_hagg):
+    x, xt, y, sh, sht, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
+    k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias, heads = ctx.meta
+    B, N, D = ctx.shape
+    dev, dt = y.device, y.dtype
+    P = c32.shape[0]
+    S = heads if heads > 1 else P
+    W = _padded_width(P, S)
+    T = B * N
+    need_x, need_wq, need_wa = ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.needs_input_grad[4]
+    tq, tb, tc, ta, tab = ctx.dtypes
+    if grad_out is None:
+        grad_out = torch.zeros(B, N, D, dtype=dt, device=dev)
+    g2 = grad_out.reshape(T, D)
+    if g2.dtype != dt:
+        g2 = g2.to(dt)
+    if not g2.is_contiguous():
+        g2 = g2.contiguous()
+    lib = _lib.load()
+    keep = [g2]
+    a = _layer_args(B, N, D, P, S, W, heads, k, frame_len, n_past, c32, b32, keep)
+    G = N // frame_len
+    wq_fits, wa_fits = _pom_gemm_fits(W, D, T), _pom_gemm_fits(D, P, T)
+    dsh = torch.empty(T, P, dtype=dt, device=dev)
+    dy = torch.empty(T, W, dtype=dt, device=dev)
+    gt = torch.empty(D, T, dtype=dt, device=dev) if need_wa and not wa_fits else None
+    dyt = torch.empty(W, T, dtype=dt, device=dev) if need_wq and not wq_fits else None
+    dx = torch.empty(T, D, dtype=dt, device=dev) if need_x else None
+    dwq = torch.empty(W, D, dtype=_wgrad_dtype(tq) if wq_fits else dt, device=dev) if need_wq else None
+    dwa = torch.empty(D, P, dtype=_wgrad_dtype(ta) if wa_fits else dt, device=dev) if need_wa else None
+    dbias = torch.empty(S, dtype=b32.dtype, device=dev)
+    dcoeff = torch.empty(P, k, dtype=c32.dtype, device=dev)
+    db_ag = torch.empty(D, dtype=torch.float32, device=dev) if has_bias else None
+    dh = torch.empty(B, G, P, dtype=torch.float32, device=dev)
+    gh = grad_hagg.float().contiguous() if grad_hagg is not None else None
+    wq_t = _weight_t(wq) if need_x else None
+    wa_t = _weight_t(wa)
+    keep.extend((wq_t, wa_t, gh))
+    a.wq, a.wq_t, a.wa, a.wa_t = wq.data_ptr(), ptr(wq_t), wa.data_ptr(), wa_t.data_ptr()
+    a.x, a.xt, a.y, a.hagg, a.count, a.sh, a.sht = (ptr(x), ptr(xt), y.data_ptr(), hagg.data_ptr(), ptr(count),
+                                                    sh.data_ptr(), ptr(sht))
+    if mask is not None:
+        a.mask, a.mask_stride_b, a.mask_stride_n = mask.data_ptr(), mask.stride(0), mask.stride(1)
+    _set_rope(a, rope_h, rope_s, keep)
+    a.g, a.gt, a.dsh, a.dy, a.dyt, a.dx = g2.data_ptr(), ptr(gt), dsh.data_ptr(), dy.data_ptr(), ptr(dyt), ptr(dx)
+    if dwq is not None:
+        a.dwq, a.dwq_dtype = dwq.data_ptr(), dtype_code(dwq)
+    if dwa is not None:
+        a.dwa, a.dwa_dtype = dwa.data_ptr(), dtype_code(dwa)
+    a.dse_bias, a.dcoeff, a.db_ag, a.dh, a.grad_hagg = (dbias.data_ptr(), dcoeff.data_ptr(), ptr(db_ag),
+                                                        dh.data_ptr(), ptr(gh))
+    ws = workspace(dev, lib.pom_layer_workspace_size(ctypes.byref(a), 1))
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    with _Span("layer_bwd"):
+        check(lib.pom_layer_bwd(ctypes.byref(a), stream_handle(dev)), "pom_layer_bwd")
+    native_layer_calls[1] += 1
+    g_carry = None
+    if has_carry:
+        w = n_past / (n_past + torch.arange(G, device=dev, dtype=torch.float32) + 1.0)
+        g_carry = (dh * w.view(1, G, 1)).sum(dim=1, keepdim=True).to(dt)
+    if dwq is not None and dwq.shape[0] != P + S:
+        dwq = dwq[:P + S]   # the padding rows' gradient is not a parameter's
+    return (None if dx is None else dx.view(B, N, D), None if dwq is None else dwq.to(tq),
+            dbias.to(tb), dcoeff.to(tc), None if dwa is None else dwa.to(ta),
+            None if db_ag is None else db_ag.to(tab), None, None, None, None, None, g_carry, None, None, None)
+
+
 class _PoMLayer(torch.autograd.Function):
     """Self-mixing PoM layer (n_groups == 1) — pom/pom.py:216-231 composed with
     _get_h_s (:204-207), pom() (:125-135) and, for RoPE, pom/pom_rope.py:476-526.
@@ -722,6 +868,29 @@ class _PoMLayer(torch.autograd.Function):
         hip_wa = training and ctx.needs_input_grad[4] and hip_gemm_fits("gemm_ag_wgrad", D, P, T, dt)
         want_xt = nt and ctx.needs_input_grad[1] and not hip_wq
         want_sht = nt and ctx.needs_input_grad[4] and not hip_wa
+        wq = _qc_weight(w_qc, dt, W)                                # (W, D), zero rows past P + S
+        c32 = _coeff_param(coeff, P, k)
+        b32 = _param(se_bias)
+        wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
+        res = None
+        if _native_layer_usable(dt, c32, b32):
+            need_q = training and ctx.needs_input_grad[1]
+            need_a = training and ctx.needs_input_grad[4]
+            res = _native_layer_forward(x2, wq, wa, b_ag, b32, c32, k, frame_len, mask, carry, n_past, rope_h,
+                                        rope_s, heads, B, N, D, P, S, W,
+                                        need_q and not _pom_gemm_fits(W, D, T),
+                                        need_a and not _pom_gemm_fits(D, P, T))
+        if res is not None:
+            y, hagg, count, sh, out, xt, sht = res
+            ctx.native = True
+            ctx.save_for_backward(x, xt, y, sh, sht, hagg, c32, b32, wq, wa, mask, count)
+            ctx.shape = (B, N, D)
+            ctx.set_materialize_grads(False)
+            ctx.meta = (k, frame_len, rope_h, rope_s, n_past, carry is not None, b_ag is not None, heads)
+            ctx.dtypes = (w_qc.dtype, se_bias.dtype, coeff.dtype, w_ag.dtype,
+                          None if b_ag is None else b_ag.dtype)
+            return out.view(B, N, D), hagg
+        ctx.native = False
         cur = torch.cuda.current_stream(dev)
         side = _copy_stream(dev) if (want_xt or want_sht) else None
         xt = sht = None
@@ -729,14 +898,11 @@ class _PoMLayer(torch.autograd.Function):
             side.wait_stream(cur)
             with torch.cuda.stream(side):
                 xt = transpose(x2, "transpose_x")                  # (D, T), overlaps qc_fwd
-        wq = _qc_weight(w_qc, dt, W)                                # (W, D), zero rows past P + S
         with _Span("gemm_qc_fwd"), tuned_gemms():
             y = torch.mm(x2, wq.t())                                # (T, W)
         y3 = y.view(B, N, W)
         h_view, s_view = y3[..., :P], y3[..., P:P + S]
-        c32 = _coeff_param(coeff, P, k)
         hagg, count = agg_forward(h_view, c32, k, frame_len, mask, carry, n_past, rope_h)
-        b32 = _param(se_bias)
         fused = want_sht and _NT_COPIES == "fused"
         if fused:
             sht = torch.empty(P, T, dtype=dt, device=dev)
@@ -748,7 +914,6 @@ class _PoMLayer(torch.autograd.Function):
             side.wait_stream(cur)
             with torch.cuda.stream(side):
                 sht = transpose(sh.view(T, P), "transpose_sh")      # (P, T), overlaps ag_fwd
-        wa = w_ag if w_ag.dtype == dt else w_ag.to(dt)
         with _Span("gemm_ag_fwd"), tuned_gemms():
             out = torch.mm(sh.view(T, P), wa.t())
         if b_ag is not None:
@@ -773,6 +938,8 @@ class _PoMLayer(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_out, grad_hagg):
+        if ctx.native:
+            return _native_layer_backward(ctx, grad_out, grad_hagg)
         x, xt, y, sh, sht, hagg, c32, b32, wq, wa, mask, count = ctx.saved_tensors
         k, frame_len, rope_h, rope_s, n_past, has_carry, has_bias, heads = ctx.meta
         B, N, D = ctx.shape

@@ -375,3 +375,22 @@ def test_gemm_plan_and_validation_before_launch(lib):
     assert call(0, 0, 256, 256, 640, 1, 0, 2) == _lib.POM_ERR_WORKSPACE       # split-K needs workspace
     assert b"workspace" in lib.pom_last_error()
     assert call(0, 0, 0, 256, 640, 1, 0, 2) == _lib.POM_OK                    # empty output: nothing to do
+
+
+def test_blas_solution_registry_validates_without_a_device():
+    """pom_blas_set_solution checks its shape and library before storing; a
+    registered shape is reported by pom_blas_has_solution; the table's "tn"
+    entries all have the K-contiguous form the layer issues."""
+    from pom_amd import _lib, gemm_select
+    lib = _lib.load()
+    assert lib.pom_blas_set_solution(0, 64, 64, 64, 64, 64, _lib.BLAS_ROCBLAS, 1) == _lib.POM_ERR_INVALID
+    assert lib.pom_blas_set_solution(64, 64, 64, 32, 64, 64, _lib.BLAS_ROCBLAS, 1) == _lib.POM_ERR_INVALID
+    assert lib.pom_blas_set_solution(64, 64, 64, 64, 64, 64, 7, 1) == _lib.POM_ERR_INVALID
+    assert lib.pom_blas_has_solution(96, 80, 72, 72, 72, 96) == 0
+    assert lib.pom_blas_set_solution(96, 80, 72, 72, 72, 96, _lib.BLAS_HIPBLASLT, 5) == _lib.POM_OK
+    assert lib.pom_blas_has_solution(96, 80, 72, 72, 72, 96) == 1
+    entries = gemm_select.table_entries()
+    lines = [ln for ln in open(gemm_select.TABLE) if ln.startswith("GemmTunableOp_BFloat16_TN,tn_")]
+    assert len(entries) == sum(",Default," not in ln for ln in lines) >= 25
+    for (m, n, k, lda, ldb, ldc), which, idx in entries:
+        assert lda == k and ldb == k and ldc == m and which in (1, 2) and idx > 0
