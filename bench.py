@@ -282,6 +282,9 @@ def gpu_run(cfg, steps, warmup, kernel_timing, graph=False):
     live = None
     if kernel_timing:
         ops._NATIVE_LAYER = False
+        for _ in range(warmup):   # the Python sequence's own first use (torch's GEMM setup)
+            step()
+        torch.cuda.synchronize()
         ops.kernel_timer = []
         for _ in range(steps):
             step()

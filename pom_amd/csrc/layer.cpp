@@ -331,6 +331,56 @@ size_t wgrad_ws(int64_t M, int64_t N, int64_t T) {
 
 int64_t groups_of(const pom_layer_args* a) { return a->N / a->frame_len; }
 
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Workspace regions, used by launches that may run at the same time on two
+// streams: [library GEMMs | dW_ag split partials | dW_qc split partials |
+// aggregation / gating / bias-gradient partials].
+struct Regions {
+  size_t wa_off = 0, wq_off = 0, rest_off = 0, total = 0;
+};
+
+// POM_AMD_LAYER_OVERLAP (read once): bit 1 runs dW_qc on a second stream
+// beside dx (both only read dY), bit 2 runs dW_ag there beside the
+// data-gradient chain (it only reads g and sh).  0 (default): one stream.
+int overlap_mode() {
+  static const int mode = [] {
+    const char* s = getenv("POM_AMD_LAYER_OVERLAP");
+    return s ? atoi(s) & 3 : 0;
+  }();
+  return mode;
+}
+
+// a second stream (default priority) and two events per device, made once
+struct Side {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+Side g_side[kMaxDevices];
+
+int side_of(Side*& out) {
+  int dev;
+  if (int r = current_device(dev)) return r;
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  Side& s = g_side[dev];
+  if (!s.stream) {
+    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess)
+      return err(POM_ERR_DEVICE, "pom_layer: second stream creation failed");
+  }
+  out = &s;
+  return POM_OK;
+}
+
+// `to` waits for everything enqueued on `from` so far
+int wait_for(hipStream_t to, hipStream_t from, hipEvent_t ev) {
+  if (hipEventRecord(ev, from) != hipSuccess || hipStreamWaitEvent(to, ev, 0) != hipSuccess)
+    return err(POM_ERR_DEVICE, "pom_layer: stream ordering failed");
+  return POM_OK;
+}
+
 // every library product of the direction has a registered solution (checked
 // before anything is launched)
 int check_solutions(const pom_layer_args* a, bool backward) {
@@ -367,6 +417,27 @@ int check_args(const pom_layer_args* a) {
   return POM_OK;
 }
 
+Regions layer_regions(const pom_layer_args* a, int backward) {
+  const int64_t T = a->B * a->N, G = groups_of(a);
+  size_t wa = 0, wq = 0, rest = 0;
+  auto upd = [](size_t& m, size_t v) { m = v > m ? v : m; };
+  upd(rest, pom_agg_workspace_size(POM_DTYPE_BF16, a->B, a->N, a->P, a->K, a->frame_len, rope_kind(a->rope_h),
+                                   backward));
+  if (a->heads > 1) upd(rest, pom_gate_heads_workspace_size(POM_DTYPE_BF16, a->B, a->N, a->P, a->heads, G));
+  else upd(rest, pom_gate_workspace_size(POM_DTYPE_BF16, a->B, a->N, a->P, G, rope_kind(a->rope_s)));
+  if (backward) {
+    wa = wgrad_ws(a->D, a->P, T);
+    wq = wgrad_ws(a->W, a->D, T);
+    upd(rest, (size_t)((T + 31) / 32) * (size_t)a->D * sizeof(float));   // bias-gradient partials
+  }
+  Regions r;
+  r.wa_off = kBlasWorkspace;
+  r.wq_off = r.wa_off + align256(wa);
+  r.rest_off = r.wq_off + align256(wq);
+  r.total = r.rest_off + align256(rest > 0 ? rest : 256);
+  return r;
+}
+
 }  // namespace
 
 extern "C" {
@@ -375,18 +446,7 @@ size_t pom_layer_args_size(void) { return sizeof(pom_layer_args); }
 
 size_t pom_layer_workspace_size(const pom_layer_args* a, int backward) {
   if (check_args(a)) return 0;
-  const int64_t T = a->B * a->N, G = groups_of(a);
-  size_t need = kBlasWorkspace;
-  auto upd = [&](size_t v) { need = v > need ? v : need; };
-  upd(pom_agg_workspace_size(POM_DTYPE_BF16, a->B, a->N, a->P, a->K, a->frame_len, rope_kind(a->rope_h), backward));
-  if (a->heads > 1) upd(pom_gate_heads_workspace_size(POM_DTYPE_BF16, a->B, a->N, a->P, a->heads, G));
-  else upd(pom_gate_workspace_size(POM_DTYPE_BF16, a->B, a->N, a->P, G, rope_kind(a->rope_s)));
-  if (backward) {
-    upd(wgrad_ws(a->D, a->P, T));
-    upd(wgrad_ws(a->W, a->D, T));
-    upd((size_t)((T + 31) / 32) * (size_t)a->D * sizeof(float));   // bias-gradient partials
-  }
-  return (need + 255) / 256 * 256;
+  return layer_regions(a, backward).total;
 }
 
 int pom_layer_fwd(const pom_layer_args* a, void* stream) {
@@ -395,19 +455,21 @@ int pom_layer_fwd(const pom_layer_args* a, void* stream) {
   if (int r = check_solutions(a, false)) return r;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t B = a->B, N = a->N, D = a->D, P = a->P, W = a->W, T = B * N, G = groups_of(a);
-  const size_t need = pom_layer_workspace_size(a, 0);
-  if (!a->workspace || a->workspace_bytes < need)
-    return err(POM_ERR_WORKSPACE, "pom_layer_fwd: workspace of %zu bytes, need %zu", a->workspace_bytes, need);
-  void* ws = a->workspace;
-  const size_t wsb = a->workspace_bytes;
+  const Regions rg = layer_regions(a, 0);
+  if (!a->workspace || a->workspace_bytes < rg.total)
+    return err(POM_ERR_WORKSPACE, "pom_layer_fwd: workspace of %zu bytes, need %zu", a->workspace_bytes, rg.total);
+  void* ws = a->workspace;   // library GEMMs
+  const size_t wsb = kBlasWorkspace;
+  void* wr = static_cast<char*>(a->workspace) + rg.rest_off;   // aggregation and gating
+  const size_t wrb = a->workspace_bytes - rg.rest_off;
   auto* y = static_cast<__hip_bfloat16*>(a->y);
   if (a->xt)
     if (int r = pom_transpose(POM_DTYPE_BF16, T, D, a->x, D, a->xt, T, stream)) return r;
   if (int r = pom::blas_gemm_tn(W, T, D, a->wq, D, a->x, D, a->y, W, ws, wsb, st)) return r;   // Y = x Wq^T
   const pom_view hv{a->y, N * W, W}, sv{y + P, N * W, W}, shv{a->sh, N * P, P};
   if (int r = pom_agg_fwd(POM_DTYPE_BF16, a->param_dtype, B, N, P, a->K, &hv, a->coeff, a->mask, a->mask_stride_b,
-                          a->mask_stride_n, a->frame_len, a->carry, a->n_past, a->rope_h, a->hagg, a->count, ws,
-                          wsb, stream))
+                          a->mask_stride_n, a->frame_len, a->carry, a->n_past, a->rope_h, a->hagg, a->count, wr,
+                          wrb, stream))
     return r;
   const pom_tview tv{a->sht, T, N};
   const pom_tview* shtv = a->sht ? &tv : nullptr;
@@ -446,21 +508,51 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   if (int r = check_solutions(a, true)) return r;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t B = a->B, N = a->N, D = a->D, P = a->P, S = a->S, W = a->W, T = B * N, G = groups_of(a);
-  const size_t need = pom_layer_workspace_size(a, 1);
-  if (!a->workspace || a->workspace_bytes < need)
-    return err(POM_ERR_WORKSPACE, "pom_layer_bwd: workspace of %zu bytes, need %zu", a->workspace_bytes, need);
-  void* ws = a->workspace;
-  const size_t wsb = a->workspace_bytes;
+  const Regions rg = layer_regions(a, 1);
+  if (!a->workspace || a->workspace_bytes < rg.total)
+    return err(POM_ERR_WORKSPACE, "pom_layer_bwd: workspace of %zu bytes, need %zu", a->workspace_bytes, rg.total);
+  void* ws = a->workspace;   // library GEMMs
+  const size_t wsb = kBlasWorkspace;
+  void* wga = static_cast<char*>(a->workspace) + rg.wa_off;   // pom_gemm split partials of dW_ag
+  const size_t wgab = rg.wq_off - rg.wa_off;
+  void* wgq = static_cast<char*>(a->workspace) + rg.wq_off;   // and of dW_qc
+  const size_t wgqb = rg.rest_off - rg.wq_off;
+  void* wr = static_cast<char*>(a->workspace) + rg.rest_off;   // streaming kernels' partials
+  const size_t wrb = a->workspace_bytes - rg.rest_off;
+  // the weight gradients that may run on the second stream (pom_gemm only)
+  const int ov = overlap_mode();
+  const bool side_wa = (ov & 2) && a->dwa && wgrad_fits(D, P, T);
+  const bool side_wq = (ov & 1) && a->dwq && wgrad_fits(W, D, T);
+  Side* sd = nullptr;
+  if (side_wa || side_wq)
+    if (int r = side_of(sd)) return r;
+  // once work is forked to the second stream, every return joins it back
+  struct Join {
+    Side* sd = nullptr;
+    hipStream_t st;
+    bool armed = false;
+    ~Join() {
+      if (armed) (void)wait_for(st, sd->stream, sd->join);
+    }
+  } join{sd, st};
   auto* y = static_cast<__hip_bfloat16*>(a->y);
   auto* dy = static_cast<__hip_bfloat16*>(a->dy);
   if (!a->wa_t) return err(POM_ERR_INVALID, "pom_layer_bwd: null wa_t");
+  // dW_ag = g^T sh, on the second stream beside the data-gradient chain
+  if (side_wa) {
+    if (int r = wait_for(sd->stream, st, sd->fork)) return r;
+    join.armed = true;
+    if (int r = pom_gemm(POM_GEMM_MN_CONTIG, POM_GEMM_MN_CONTIG, D, P, T, a->g, D, a->sh, P, a->dwa_dtype, a->dwa, P,
+                         -1, 0, wga, wgab, sd->stream))
+      return r;
+  }
   // dsh = g Wa
   if (int r = pom::blas_gemm_tn(P, T, D, a->wa_t, D, a->g, D, a->dsh, P, ws, wsb, st)) return r;
   // dW_ag = g^T sh
-  if (a->dwa) {
+  if (a->dwa && !side_wa) {
     if (wgrad_fits(D, P, T)) {
       if (int r = pom_gemm(POM_GEMM_MN_CONTIG, POM_GEMM_MN_CONTIG, D, P, T, a->g, D, a->sh, P, a->dwa_dtype, a->dwa,
-                           P, -1, 0, ws, wsb, stream))
+                           P, -1, 0, wga, wgab, stream))
         return r;
     } else {
       if (!a->gt || !a->sht || a->dwa_dtype != POM_DTYPE_BF16)
@@ -472,7 +564,7 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   // db_ag = sum over tokens of g, in fp32
   if (a->db_ag) {
     const int64_t rc = 32, nch = (T + rc - 1) / rc;
-    float* part = static_cast<float*>(ws);
+    float* part = static_cast<float*>(wr);
     const dim3 gp((unsigned)((D + kThreadsL - 1) / kThreadsL), (unsigned)nch);
     hipLaunchKernelGGL(col_sum_part, gp, dim3(kThreadsL), 0, st, static_cast<const __hip_bfloat16*>(a->g), T, D, rc,
                        part);
@@ -487,7 +579,7 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   const pom_view sv{y + P, N * W, W}, dshv{a->dsh, N * P, P}, dysv{dy + P, N * W, W};
   if (a->heads > 1) {
     if (int r = pom_gate_heads_bwd(POM_DTYPE_BF16, a->param_dtype, B, N, P, a->heads, &sv, a->se_bias, a->hagg, G,
-                                   a->rope_s, &dshv, &dysv, a->dh, a->dse_bias, ws, wsb, stream))
+                                   a->rope_s, &dshv, &dysv, a->dh, a->dse_bias, wr, wrb, stream))
       return r;
     if (a->dyt)   // the gate rows of dY^T (with the padding rows)
       if (int r = pom_transpose(POM_DTYPE_BF16, T, W - P, dy + P, W, static_cast<__hip_bfloat16*>(a->dyt) + P * T, T,
@@ -496,10 +588,10 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   } else {
     const pom_tview tv{a->dyt ? static_cast<__hip_bfloat16*>(a->dyt) + P * T : nullptr, T, N};
     int r = pom_gate_bwd(POM_DTYPE_BF16, a->param_dtype, B, N, P, &sv, a->se_bias, a->hagg, G, a->rope_s, &dshv,
-                         &dysv, a->dyt ? &tv : nullptr, a->dh, a->dse_bias, ws, wsb, stream);
+                         &dysv, a->dyt ? &tv : nullptr, a->dh, a->dse_bias, wr, wrb, stream);
     if (r == POM_ERR_UNSUPPORTED && a->dyt) {
       r = pom_gate_bwd(POM_DTYPE_BF16, a->param_dtype, B, N, P, &sv, a->se_bias, a->hagg, G, a->rope_s, &dshv,
-                       &dysv, nullptr, a->dh, a->dse_bias, ws, wsb, stream);
+                       &dysv, nullptr, a->dh, a->dse_bias, wr, wrb, stream);
       if (!r) r = pom_transpose(POM_DTYPE_BF16, T, S, dy + P, W, static_cast<__hip_bfloat16*>(a->dyt) + P * T, T,
                                 stream);
     }
@@ -514,14 +606,22 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
     const pom_tview tv{a->dyt, T, N};
     int r = pom_agg_bwd(POM_DTYPE_BF16, a->param_dtype, B, N, P, a->K, &hv, a->coeff, a->mask, a->mask_stride_b,
                         a->mask_stride_n, a->count, a->frame_len, a->n_past, a->rope_h, a->dh, &dhv,
-                        a->dyt ? &tv : nullptr, a->dcoeff, ws, wsb, stream);
+                        a->dyt ? &tv : nullptr, a->dcoeff, wr, wrb, stream);
     if (r == POM_ERR_UNSUPPORTED && a->dyt) {
       r = pom_agg_bwd(POM_DTYPE_BF16, a->param_dtype, B, N, P, a->K, &hv, a->coeff, a->mask, a->mask_stride_b,
                       a->mask_stride_n, a->count, a->frame_len, a->n_past, a->rope_h, a->dh, &dhv, nullptr,
-                      a->dcoeff, ws, wsb, stream);
+                      a->dcoeff, wr, wrb, stream);
       if (!r) r = pom_transpose(POM_DTYPE_BF16, T, P, a->dy, W, a->dyt, T, stream);
     }
     if (r) return r;
+  }
+  // dW_qc = dY^T x on the second stream beside dx (both only read dY)
+  if (side_wq) {
+    if (int r = wait_for(sd->stream, st, sd->fork)) return r;
+    join.armed = true;
+    if (int r = pom_gemm(POM_GEMM_MN_CONTIG, POM_GEMM_MN_CONTIG, W, D, T, a->dy, W, a->x, D, a->dwq_dtype, a->dwq, D,
+                         -1, 0, wgq, wgqb, sd->stream))
+      return r;
   }
   // dx = dY Wq
   if (a->dx) {
@@ -529,16 +629,20 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
     if (int r = pom::blas_gemm_tn(D, T, W, a->wq_t, W, a->dy, W, a->dx, D, ws, wsb, st)) return r;
   }
   // dW_qc = dY^T x
-  if (a->dwq) {
+  if (a->dwq && !side_wq) {
     if (wgrad_fits(W, D, T)) {
       if (int r = pom_gemm(POM_GEMM_MN_CONTIG, POM_GEMM_MN_CONTIG, W, D, T, a->dy, W, a->x, D, a->dwq_dtype, a->dwq,
-                           D, -1, 0, ws, wsb, stream))
+                           D, -1, 0, wgq, wgqb, stream))
         return r;
     } else {
       if (!a->xt || !a->dyt || a->dwq_dtype != POM_DTYPE_BF16)
         return err(POM_ERR_INVALID, "pom_layer_bwd: dW_qc off pom_gemm needs xt, dyt and a bf16 output");
       if (int r = pom::blas_gemm_tn(D, W, T, a->xt, T, a->dyt, T, a->dwq, D, ws, wsb, st)) return r;
     }
+  }
+  if (join.armed) {   // the caller's stream sees the second stream's work done
+    join.armed = false;
+    if (int r = wait_for(st, sd->stream, sd->join)) return r;
   }
   return POM_OK;
 }
