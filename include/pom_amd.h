@@ -273,8 +273,12 @@ int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_
  * aligned.  tile < 0 and splits <= 0 choose both from the shape
  * (pom_gemm_plan).  splits > 1 divides K into that many contiguous parts
  * whose fp32 partials are summed in a fixed order (deterministic), using
- * pom_gemm_workspace_size() bytes of workspace. */
+ * pom_gemm_workspace_size() bytes of workspace.  splits == POM_GEMM_STREAM_K
+ * shares the tiles' 64-steps evenly among 256 workgroups (one per CU), so a
+ * workgroup's range may cover parts of two tiles; the fp32 tile partials are
+ * summed in a fixed order too (needs tiles x K / 64 >= 256). */
 typedef enum { POM_GEMM_K_CONTIG = 0, POM_GEMM_MN_CONTIG = 1 } pom_gemm_layout;
+#define POM_GEMM_STREAM_K 256
 #define POM_GEMM_TILES 6   /* tile ids: 256x256, 256x192, 192x256, 256x128, 128x256, 128x128 (BM x BN) */
 
 /* The tile and split count pom_gemm uses for this shape and these layouts

@@ -110,6 +110,7 @@ SIGNATURES = {
     "pom_layer_bwd": (_c_int, [ctypes.POINTER(PomLayerArgs), _c_vp]),
 }
 BLAS_ROCBLAS, BLAS_HIPBLASLT = 1, 2
+GEMM_STREAM_K = 256   # pom_gemm's `splits` value for the stream-K schedule
 
 _lib: Optional[ctypes.CDLL] = None
 _lib_lock = threading.Lock()

@@ -922,22 +922,52 @@ bool gemm_tile_fits(int64_t M, int64_t N, int tile) {
   return M % bm == 0 && N % bn == 0;
 }
 
+size_t gemm_ws_bytes(int64_t M, int64_t N, int tile, int splits) {
+  if (splits == pom::GEMM_STREAM_K) {
+    int bm, bn;
+    pom::gemm_tile_dims(tile, &bm, &bn);
+    return pom::gemm_streamk_ws_bytes(M, N, bm, bn);
+  }
+  return splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * 4 : 0;
+}
+
+// stream-K needs at least one 64-step per workgroup
+bool gemm_streamk_fits(int64_t M, int64_t N, int64_t K, int tile) {
+  int bm, bn;
+  pom::gemm_tile_dims(tile, &bm, &bn);
+  return (M / bm) * (N / bn) * (K / 64) >= pom::kStreamKGroups;
+}
+
 // Measured best (tile, splits) for the weight-gradient products of the baseline configurations
-// (M/N-contiguous operands; MI355X, isolated runs over every tile and 1-8 splits).
+// (M/N-contiguous operands; MI355X, isolated runs over every tile and 1-8 splits, then stream-K
+// against that choice inside the layer's backward, same box, alternating).  Stream-K's workgroups
+// start at different k offsets, so the CUs of one XCD no longer read the same operand slices
+// together, and the L2 reuse of the lockstep split-K grid is lost.  In the layer that costs more
+// than the idle CUs it fills everywhere but config 4's dW_qc (882-887 us against 908-912); e.g.
+// config 5's dW_qc 677-681 against 609-612, config 2 isolated 236 against 202.
+// sk_tile >= 0: stream-K on that tile, unless POM_AMD_GEMM_STREAMK=0 asks for (tile, splits).
 struct GemmTuned {
   int64_t M, N, K;
-  int a_layout, b_layout, tile, splits;
+  int a_layout, b_layout, tile, splits, sk_tile;
 };
 const GemmTuned kGemmTuned[] = {
-    {1152, 2304, 16384, 1, 1, 2, 4},  // config 2: dW_ag = g^T sh
-    {4608, 1152, 16384, 1, 1, 1, 2},  // config 2: dW_qc = dY^T x
-    {1024, 2048, 65536, 1, 1, 0, 8},  // config 3
-    {4096, 1024, 65536, 1, 1, 0, 4},
-    {1024, 4096, 65536, 1, 1, 0, 4},  // config 4
-    {8192, 1024, 65536, 1, 1, 0, 4},
-    {1536, 3072, 32768, 1, 1, 0, 7},  // config 5
-    {6144, 1536, 32768, 1, 1, 0, 3},
+    {1152, 2304, 16384, 1, 1, 2, 4, -1},  // config 2: dW_ag = g^T sh
+    {4608, 1152, 16384, 1, 1, 1, 2, -1},  // config 2: dW_qc = dY^T x
+    {1024, 2048, 65536, 1, 1, 0, 8, -1},  // config 3
+    {4096, 1024, 65536, 1, 1, 0, 4, -1},
+    {1024, 4096, 65536, 1, 1, 0, 4, -1},  // config 4
+    {8192, 1024, 65536, 1, 1, 0, 4, 0},
+    {1536, 3072, 32768, 1, 1, 0, 7, -1},  // config 5
+    {6144, 1536, 32768, 1, 1, 0, 3, -1},
 };
+
+bool streamk_allowed() {
+  static const bool on = [] {
+    const char* e = getenv("POM_AMD_GEMM_STREAMK");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
 
 // POM_AMD_GEMM_FORCE="tile,splits" pins the choice (tile sweeps); then the measured table; then the
 // cost model.
@@ -946,8 +976,9 @@ GemmCost gemm_choose(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout
   static const char* force = getenv("POM_AMD_GEMM_FORCE");
   if (force) {
     int t = -1, sp = 1;
-    if (sscanf(force, "%d,%d", &t, &sp) == 2 && t >= 0 && t < pom::GEMM_TILE_COUNT && sp >= 1 &&
-        sp <= kGemmMaxSplits && gemm_tile_fits(M, N, t) && K / 64 >= sp) {
+    if (sscanf(force, "%d,%d", &t, &sp) == 2 && t >= 0 && t < pom::GEMM_TILE_COUNT && gemm_tile_fits(M, N, t) &&
+        ((sp >= 1 && sp <= kGemmMaxSplits && K / 64 >= sp) ||
+         (sp == pom::GEMM_STREAM_K && gemm_streamk_fits(M, N, K, t)))) {
       best.tile = t;
       best.splits = sp;
       best.us = 0;
@@ -956,8 +987,9 @@ GemmCost gemm_choose(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout
   }
   for (const GemmTuned& e : kGemmTuned) {
     if (e.M == M && e.N == N && e.K == K && e.a_layout == a_layout && e.b_layout == b_layout) {
-      best.tile = e.tile;
-      best.splits = e.splits;
+      const bool sk = e.sk_tile >= 0 && streamk_allowed();
+      best.tile = sk ? e.sk_tile : e.tile;
+      best.splits = sk ? pom::GEMM_STREAM_K : e.splits;
       best.us = 0;
       return best;
     }
@@ -971,10 +1003,6 @@ GemmCost gemm_choose(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout
     }
   }
   return best;
-}
-
-size_t gemm_ws_bytes(int64_t M, int64_t N, int splits) {
-  return splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * 4 : 0;
 }
 
 }  // namespace
@@ -998,12 +1026,13 @@ size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int sp
       for (int bl = 0; bl < 2; ++bl) {
         int t = -1, sp = 1;
         if (pom_gemm_plan(M, N, K, al, bl, &t, &sp) != POM_OK) return 0;
-        const size_t b = gemm_ws_bytes(M, N, splits <= 0 ? sp : splits);
+        const size_t b = gemm_ws_bytes(M, N, t, splits <= 0 ? sp : splits);
         need = b > need ? b : need;
       }
     return need;
   }
-  return gemm_ws_bytes(M, N, splits);
+  if (tile >= pom::GEMM_TILE_COUNT) return 0;
+  return gemm_ws_bytes(M, N, tile, splits);
 }
 
 int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
@@ -1032,11 +1061,16 @@ int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const 
   }
   if (tile < 0 || tile >= pom::GEMM_TILE_COUNT || !gemm_tile_fits(M, N, tile))
     return fail(POM_ERR_UNSUPPORTED, "gemm: tile %d does not divide M=%lld, N=%lld", tile, (long long)M, (long long)N);
-  if (splits > kGemmMaxSplits || splits > K / 64)
-    return fail(POM_ERR_UNSUPPORTED, "gemm: splits (%d) must be <= %d and <= K / 64", splits, kGemmMaxSplits);
+  if (splits == pom::GEMM_STREAM_K) {
+    if (!gemm_streamk_fits(M, N, K, tile))
+      return fail(POM_ERR_UNSUPPORTED, "gemm: stream-K needs tiles x K / 64 >= %d", pom::kStreamKGroups);
+  } else if (splits > kGemmMaxSplits || splits > K / 64) {
+    return fail(POM_ERR_UNSUPPORTED, "gemm: splits (%d) must be <= %d and <= K / 64, or POM_GEMM_STREAM_K", splits,
+                kGemmMaxSplits);
+  }
   if (M * N > ((int64_t)1 << 31) || M > INT32_MAX || N > INT32_MAX || K / 64 > INT32_MAX)
     return fail(POM_ERR_UNSUPPORTED, "gemm: output too large");
-  const size_t need = gemm_ws_bytes(M, N, splits);
+  const size_t need = gemm_ws_bytes(M, N, tile, splits);
   if (need && (!workspace || workspace_bytes < need || !aligned(workspace, 16)))
     return fail(POM_ERR_WORKSPACE, "gemm: workspace of %zu bytes (16-byte aligned) needed, got %zu", need,
                 workspace ? workspace_bytes : (size_t)0);

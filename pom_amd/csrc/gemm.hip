@@ -37,6 +37,14 @@
 //   * split-K: the k range is cut into S contiguous parts (whole 64-steps),
 //     each written as an fp32 partial (S, M, N); gemm_splitk_reduce sums the
 //     partials in split order, so results do not depend on scheduling;
+//   * stream-K: G workgroups (one per CU) share the tiles' 64-steps evenly.
+//     Workgroup w takes the global steps [w I / G, (w + 1) I / G) of the
+//     I = tiles x steps in tile order, so its range may end inside one tile
+//     and continue into the next; each (tile t, workgroup w) segment writes
+//     an fp32 tile partial into slot t + w (distinct for every segment, as
+//     each next segment advances t, w or both), and gemm_streamk_reduce sums
+//     a tile's segments in workgroup order (deterministic).  This fills every
+//     CU when tiles x splits would leave some idle;
 //   * workgroups are dispatched to the 8 XCDs round-robin; the grid index is
 //     remapped so each XCD owns a contiguous run of tiles, ordered in groups
 //     of GM row tiles, and its 32 CUs share operand panels in their L2.
@@ -71,6 +79,33 @@ struct GemmArgs {
   int splits;
   int tiles_m, tiles_n;
 };
+
+// Stream-K segments of tile t: the first and last workgroup whose step range
+// meets the tile's steps [t nk, (t + 1) nk), for G workgroups over I steps
+// (workgroup w owns [floor(w I / G), floor((w + 1) I / G)), never empty as I >= G).
+__host__ __device__ inline int64_t sk_first(int64_t t, int64_t nk, int64_t I, int64_t G) {
+  return (((t * nk + 1) * G + I - 1) / I) - 1;
+}
+__host__ __device__ inline int64_t sk_last(int64_t t, int64_t nk, int64_t I, int64_t G) {
+  return ((((t + 1) * nk) * G + I - 1) / I) - 1;
+}
+
+// row tile and column tile of tile index t: tiles run in groups of kGroupM row tiles, column-major
+// within a group, so consecutive workgroups share operand panels
+__host__ __device__ inline void tile_coords(int t, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int span = kGroupM * tiles_n;
+  const int grp = t / span;
+  const int first_m = grp * kGroupM;
+  const int gsz = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  t -= grp * span;
+  tm = first_m + t % gsz;
+  tn = t / gsz;
+}
+__host__ __device__ inline int tile_index(int tm, int tn, int tiles_m, int tiles_n) {
+  const int grp = tm / kGroupM, first_m = grp * kGroupM;
+  const int gsz = tiles_m - first_m < kGroupM ? tiles_m - first_m : kGroupM;
+  return grp * kGroupM * tiles_n + tn * gsz + (tm - first_m);
+}
 
 // LDS bytes of one operand's sub-array (one 16-k sub-step) and of the operand.
 template <int R>
@@ -171,32 +206,19 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <int BM, int BN, bool A_MN, bool B_MN, bool OUT_F32>
-__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
+// One output tile over the 64-steps [it0, it1): C(m, n) at c + (m - LOCAL ? m0 : 0) * ldc + (n - LOCAL ? n0 : 0).
+template <int BM, int BN, bool A_MN, bool B_MN, bool OUT_F32, bool LOCAL>
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int t, int it0, int it1, void* cout,
+                                          int64_t ldc) {
   constexpr int WM = BM / 2, WN = BN / 2, MB = WM / 32, NB = WN / 32;
   constexpr int A_BYTES = opnd_bytes<BM>(), STAGE = opnd_bytes<BM>() + opnd_bytes<BN>();
   static_assert(MB >= 1 && NB >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile");
-  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-
-  // grid index -> (split, row tile, column tile)
-  const int total = (int)gridDim.x;
-  int bid = (int)blockIdx.x;
-  if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-  const int ntile = g.tiles_m * g.tiles_n;
-  const int split = bid / ntile;
-  int t = bid - split * ntile;
-  const int span = kGroupM * g.tiles_n;
-  const int grp = t / span;
-  const int first_m = grp * kGroupM;
-  const int gsz = min(kGroupM, g.tiles_m - first_m);
-  t -= grp * span;
-  const int tm = first_m + t % gsz, tn = t / gsz;
+  int tm, tn;
+  tile_coords(t, g.tiles_m, g.tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const int it0 = (int)(((int64_t)split * g.nk) / g.splits);
-  const int it1 = (int)(((int64_t)(split + 1) * g.nk) / g.splits);
   const int nk = it1 - it0;
   const int kbeg = it0 * kBK;
 
@@ -316,18 +338,18 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
   // epilogue: lane holds C[m = mrow][n = n0 + ... + 8q + 4 * lhalf + (0..3)] in acc[i][j][4q .. 4q+3]
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
-    const int64_t m = m0 + wm * WM + 32 * i + lrow;
+    const int64_t m = (LOCAL ? 0 : m0) + wm * WM + 32 * i + lrow;
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WN + 32 * j + 8 * q + 4 * lhalf;
+        const int n = (LOCAL ? 0 : n0) + wn * WN + 32 * j + 8 * q + 4 * lhalf;
         if constexpr (OUT_F32) {
-          float* c = static_cast<float*>(g.C) + (int64_t)split * g.split_stride + m * g.ldc + n;
+          float* c = static_cast<float*>(cout) + m * ldc + n;
           f32x4_t v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
           *reinterpret_cast<f32x4_t*>(c) = v;
         } else {
-          uint16_t* c = static_cast<uint16_t*>(g.C) + m * g.ldc + n;
+          uint16_t* c = static_cast<uint16_t*>(cout) + m * ldc + n;
           f32x2_t lo = {acc[i][j][4 * q], acc[i][j][4 * q + 1]};
           f32x2_t hi = {acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
           bf16x2_t blo = __builtin_convertvector(lo, bf16x2_t);
@@ -337,6 +359,38 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
         }
       }
     }
+  }
+}
+
+// SK false: one workgroup per (split, tile); true: the stream-K schedule over gridDim.x workgroups.
+template <int BM, int BN, bool A_MN, bool B_MN, bool OUT_F32, bool SK>
+__global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
+  constexpr int STAGE = opnd_bytes<BM>() + opnd_bytes<BN>();
+  __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
+  // workgroups reach the 8 XCDs round-robin: give each XCD a contiguous run of work
+  const int total = (int)gridDim.x;
+  int bid = (int)blockIdx.x;
+  if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  const int ntile = g.tiles_m * g.tiles_n;
+  if constexpr (SK) {
+    const int64_t I = (int64_t)ntile * g.nk, G = total;
+    int64_t lo = (int64_t)bid * I / G;
+    const int64_t hi = ((int64_t)bid + 1) * I / G;
+    while (lo < hi) {
+      const int t = (int)(lo / g.nk);
+      const int64_t end = min(hi, ((int64_t)t + 1) * g.nk);
+      float* part = static_cast<float*>(g.C) + ((int64_t)t + bid) * (BM * BN);
+      gemm_tile<BM, BN, A_MN, B_MN, true, true>(g, smem, t, (int)(lo - (int64_t)t * g.nk),
+                                                (int)(end - (int64_t)t * g.nk), part, BN);
+      lo = end;
+    }
+  } else {
+    const int split = bid / ntile;
+    const int t = bid - split * ntile;
+    const int it0 = (int)(((int64_t)split * g.nk) / g.splits);
+    const int it1 = (int)(((int64_t)(split + 1) * g.nk) / g.splits);
+    void* c = OUT_F32 ? static_cast<void*>(static_cast<float*>(g.C) + (int64_t)split * g.split_stride) : g.C;
+    gemm_tile<BM, BN, A_MN, B_MN, OUT_F32, false>(g, smem, t, it0, it1, c, g.ldc);
   }
 }
 
@@ -371,13 +425,55 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float* __restric
   }
 }
 
+// out[m, n] = sum over the stream-K segments of (m, n)'s tile, in workgroup order; 8 outputs per thread
+// (BN is a multiple of 8, so they share a tile).
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void gemm_streamk_reduce(const float* __restrict__ part, int bm, int bn,
+                                                           int tiles_m, int tiles_n, int nk, int groups, int M,
+                                                           int N, void* __restrict__ out, int64_t ldo) {
+  const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (idx >= (int64_t)M * N) return;
+  const int m = (int)(idx / N), n = (int)(idx - (int64_t)m * N);
+  const int tm = m / bm, tn = n / bn;
+  const int64_t t = tile_index(tm, tn, tiles_m, tiles_n);
+  const int64_t I = (int64_t)tiles_m * tiles_n * nk;
+  const int64_t w0 = sk_first(t, nk, I, groups), w1 = sk_last(t, nk, I, groups);
+  const int64_t tsz = (int64_t)bm * bn;
+  const float* p = part + (t + w0) * tsz + (int64_t)(m - tm * bm) * bn + (n - tn * bn);
+  f32x4_t a = *reinterpret_cast<const f32x4_t*>(p), b = *reinterpret_cast<const f32x4_t*>(p + 4);
+  for (int64_t w = w0 + 1; w <= w1; ++w) {
+    p += tsz;
+    a += *reinterpret_cast<const f32x4_t*>(p);
+    b += *reinterpret_cast<const f32x4_t*>(p + 4);
+  }
+  if constexpr (OUT_F32) {
+    float* o = static_cast<float*>(out) + (int64_t)m * ldo + n;
+    *reinterpret_cast<f32x4_t*>(o) = a;
+    *reinterpret_cast<f32x4_t*>(o + 4) = b;
+  } else {
+    u32x4_t wv;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      f32x2_t x = {a[2 * e], a[2 * e + 1]}, y = {b[2 * e], b[2 * e + 1]};
+      wv[e] = __builtin_bit_cast(unsigned, __builtin_convertvector(x, bf16x2_t));
+      wv[e + 2] = __builtin_bit_cast(unsigned, __builtin_convertvector(y, bf16x2_t));
+    }
+    *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(out) + (int64_t)m * ldo + n) = wv;
+  }
+}
+
 template <int BM, int BN, bool A_MN, bool B_MN>
 hipError_t launch_tile(const GemmArgs& g, bool out_f32, hipStream_t st) {
+  if (g.splits == GEMM_STREAM_K) {
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, A_MN, B_MN, true, true>), dim3(kStreamKGroups), dim3(kThreads), 0,
+                       st, g);
+    return hipGetLastError();
+  }
   const dim3 grid((unsigned)(g.tiles_m * g.tiles_n * g.splits));
   if (out_f32)
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, A_MN, B_MN, true>), grid, dim3(kThreads), 0, st, g);
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, A_MN, B_MN, true, false>), grid, dim3(kThreads), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, A_MN, B_MN, false>), grid, dim3(kThreads), 0, st, g);
+    hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, A_MN, B_MN, false, false>), grid, dim3(kThreads), 0, st, g);
   return hipGetLastError();
 }
 
@@ -418,9 +514,14 @@ hipError_t gemm_bf16(const GemmProblem& p, hipStream_t st) {
   g.splits = p.splits;
   g.tiles_m = (int)(p.M / bm);
   g.tiles_n = (int)(p.N / bn);
+  const bool sk = p.splits == GEMM_STREAM_K;
   const bool direct = p.splits == 1;
   const bool f32 = p.out_f32 || !direct;
-  if (direct) {
+  if (sk) {
+    g.C = p.workspace;
+    g.ldc = bn;
+    g.split_stride = 0;
+  } else if (direct) {
     g.C = p.C;
     g.ldc = p.ldc;
     g.split_stride = 0;
@@ -440,6 +541,15 @@ hipError_t gemm_bf16(const GemmProblem& p, hipStream_t st) {
   if (e != hipSuccess || direct) return e;
   const int64_t n8 = p.M * p.N / 8;
   const dim3 grid((unsigned)((n8 + 255) / 256));
+  if (sk) {
+    if (p.out_f32)
+      hipLaunchKernelGGL((gemm_streamk_reduce<true>), grid, dim3(256), 0, st, static_cast<const float*>(p.workspace),
+                         bm, bn, g.tiles_m, g.tiles_n, g.nk, kStreamKGroups, g.M, g.N, p.C, p.ldc);
+    else
+      hipLaunchKernelGGL((gemm_streamk_reduce<false>), grid, dim3(256), 0, st, static_cast<const float*>(p.workspace),
+                         bm, bn, g.tiles_m, g.tiles_n, g.nk, kStreamKGroups, g.M, g.N, p.C, p.ldc);
+    return hipGetLastError();
+  }
   if (p.out_f32)
     hipLaunchKernelGGL((gemm_splitk_reduce<true>), grid, dim3(256), 0, st, static_cast<const float*>(p.workspace),
                        g.split_stride, p.splits, g.M, g.N, p.C, p.ldc);

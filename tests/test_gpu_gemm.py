@@ -1,7 +1,8 @@
 """pom_gemm (the matrix-core projection GEMM) against torch's fp32 product of
 the same bf16 operands: every operand layout, tile, split count and output
-dtype, pipeline lengths 1-5 and 16 steps, padded leading dimensions, strided
-views, the C2 weight-gradient shapes at full size, and determinism."""
+dtype, pipeline lengths 1-5 and 16 steps, the stream-K schedule, padded
+leading dimensions, strided views, the C2 weight-gradient shapes at full
+size, and determinism."""
 import ctypes
 
 import pytest
@@ -128,10 +129,41 @@ def test_gemm_deterministic_with_splits(device):
         assert torch.equal(c1, c2)
 
 
+@pytest.mark.parametrize("a_mn,b_mn", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("tile", sorted(TILES))
+def test_gemm_stream_k_layouts_and_tiles(device, a_mn, b_mn, tile):
+    """Stream-K: 256 workgroups over 6 tiles x nk steps.  nk = 43 gives
+    segments of one or two steps (many workgroups per tile), 100 and 171
+    ranges that end inside a tile and carry on into the next; 256 puts every
+    workgroup boundary at a multiple of a sixth of a tile."""
+    bm, bn = TILES[tile]
+    M, N = 3 * bm, 2 * bn
+    for nk in (43, 100, 171, 256):
+        K = 64 * nk
+        a, b = _operands(M, N, K, a_mn, b_mn, device, seed=nk + 7 * tile)
+        ref = _reference(a, a_mn, b, b_mn)
+        for out_dtype in (torch.bfloat16, torch.float32):
+            c = _run(a, a_mn, b, b_mn, M, N, K, out_dtype, tile, _lib.GEMM_STREAM_K)
+            _check(c, ref, out_dtype, f"stream-K tile {bm}x{bn} A{int(a_mn)} B{int(b_mn)} nk{nk} {out_dtype}")
+
+
+def test_gemm_stream_k_deterministic_and_padded(device):
+    M, N, K = 768, 512, 4096
+    a, b = _operands(M, N, K, True, True, device, seed=13, pad=40)
+    ref = _reference(a, True, b, True)
+    for tile in (0, 5):
+        if M % TILES[tile][0] or N % TILES[tile][1]:
+            continue
+        c1 = _run(a, True, b, True, M, N, K, torch.float32, tile, _lib.GEMM_STREAM_K)
+        c2 = _run(a, True, b, True, M, N, K, torch.float32, tile, _lib.GEMM_STREAM_K)
+        assert torch.equal(c1, c2)
+        _check(c1, ref, torch.float32, f"stream-K padded tile {tile}")
+
+
 def test_gemm_plan_chooses_a_dividing_tile(device):
     lib = _lib.load()
     for (M, N, K) in ((16384, 4608, 1152), (1152, 2304, 16384), (4608, 1152, 16384), (65536, 1024, 4096)):
         t, s = ctypes.c_int(), ctypes.c_int()
         assert lib.pom_gemm_plan(M, N, K, 0, 0, ctypes.byref(t), ctypes.byref(s)) == 0
         bm, bn = TILES[t.value]
-        assert M % bm == 0 and N % bn == 0 and 1 <= s.value <= K // 64
+        assert M % bm == 0 and N % bn == 0 and (1 <= s.value <= K // 64 or s.value == _lib.GEMM_STREAM_K)
