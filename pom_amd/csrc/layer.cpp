@@ -340,15 +340,13 @@ struct Regions {
   size_t wa_off = 0, wq_off = 0, rest_off = 0, total = 0;
 };
 
-// POM_AMD_LAYER_OVERLAP (read once): bit 1 runs dW_qc on a second stream
-// beside dx (both only read dY), bit 2 runs dW_ag there beside the
-// data-gradient chain (it only reads g and sh).  0 (default): one stream.
+// POM_AMD_LAYER_OVERLAP (read at every backward call, a few hundred ns): bit 1
+// runs dW_qc on a second stream beside dx (both only read dY), bit 2 runs dW_ag
+// there beside the data-gradient chain (it only reads g and sh).  0 (default):
+// one stream.
 int overlap_mode() {
-  static const int mode = [] {
-    const char* s = getenv("POM_AMD_LAYER_OVERLAP");
-    return s ? atoi(s) & 3 : 0;
-  }();
-  return mode;
+  const char* s = getenv("POM_AMD_LAYER_OVERLAP");
+  return s ? atoi(s) & 3 : 0;
 }
 
 // a second stream (default priority) and two events per device, made once

@@ -53,3 +53,29 @@ def test_native_layer_matches_python_sequence(device, monkeypatch, name, bias):
             assert bool(((a - b).abs() <= b.abs() * 2.0 ** -7 + 1e-6).all()), n
         else:
             assert torch.equal(gp_n[n], gp_p[n]), n
+
+
+@pytest.mark.parametrize("name", ["c2", "c5"])
+def test_native_backward_second_stream_is_bit_identical(device, monkeypatch, name):
+    """POM_AMD_LAYER_OVERLAP (read by pom_layer_bwd at each call) runs dW_qc
+    beside dx and / or dW_ag beside the data-gradient chain on a second stream,
+    each with its own split-K workspace; the caller's stream waits for that
+    stream before the call returns.  Every gradient equals the one-stream run's."""
+    if not gemm_select.native_ready():
+        pytest.skip("the C library does not resolve to torch's rocBLAS / hipBLASLt, or torch rejected the table")
+    cfg = bench.CONFIGS[name]
+    x, go, extra = bench.make_inputs(cfg)
+    m = bench.make_module(cfg).to(device, torch.bfloat16)
+    fwd = bench.forward_fn(cfg, {k: v.to(device) for k, v in extra.items()})
+    x, go = x.to(device, torch.bfloat16), go.to(device, torch.bfloat16)
+    monkeypatch.setattr(ops, "_NATIVE_LAYER", True)
+    monkeypatch.setenv("POM_AMD_LAYER_OVERLAP", "0")
+    ref = _run(m, fwd, x, go)
+    for mode in ("1", "2", "3"):
+        monkeypatch.setenv("POM_AMD_LAYER_OVERLAP", mode)
+        calls = ops.native_layer_calls[1]
+        got = _run(m, fwd, x, go)
+        assert ops.native_layer_calls[1] == calls + 1, "the C sequence did not run"
+        assert torch.equal(got[0], ref[0]) and torch.equal(got[1], ref[1]), f"mode {mode}: output / grad_x"
+        for n in ref[2]:
+            assert torch.equal(got[2][n], ref[2][n]), f"mode {mode}: {n}"
