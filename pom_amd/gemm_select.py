@@ -12,7 +12,8 @@ benchmarked or written at run time.  Shapes missing from the table use the
 default heuristic.  The table is rejected by torch (and the default used) when
 the PyTorch, ROCm, hipBLASLt or rocBLAS versions differ from the ones it was
 made with.  The caller's TunableOp settings are restored on exit.  Set
-POM_AMD_TUNED_GEMMS=0 to disable.
+POM_AMD_TUNED_GEMMS=0 to disable, or POM_AMD_GEMM_TABLE to the path of another
+table in the same format.
 """
 from __future__ import annotations
 
@@ -22,7 +23,7 @@ import threading
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-TABLE = os.path.join(_HERE, "tuned", "gemm_gfx950.csv")
+TABLE = os.environ.get("POM_AMD_GEMM_TABLE") or os.path.join(_HERE, "tuned", "gemm_gfx950.csv")
 
 _lock = threading.Lock()
 _loaded = None   # None: not tried; True/False: table usable
