@@ -268,9 +268,10 @@ int pom_transpose(int dtype, int64_t rows, int64_t cols, const void* src, int64_
  *   b_layout POM_GEMM_K_CONTIG : B(k, n) = B[n * ldb + k]   (an nn.Linear weight, y = x W^T)
  *            POM_GEMM_MN_CONTIG: B(k, n) = B[k * ldb + n]
  * out_dtype: POM_DTYPE_BF16 (round to nearest even) or POM_DTYPE_F32.
- * Requirements (else POM_ERR_UNSUPPORTED): M, N multiples of the chosen
- * tile, K a multiple of 64, operands and leading dimensions 16-byte
- * aligned.  tile < 0 and splits <= 0 choose both from the shape
+ * Requirements (else POM_ERR_UNSUPPORTED): M, N multiples of 8 (a tile
+ * that does not divide them leaves a partial last tile, whose rows and
+ * columns past M / N are not stored), K a multiple of 64, operands and
+ * leading dimensions 16-byte aligned.  tile < 0 and splits <= 0 choose both from the shape
  * (pom_gemm_plan).  splits > 1 divides K into that many contiguous parts
  * whose fp32 partials are summed in a fixed order (deterministic), using
  * pom_gemm_workspace_size() bytes of workspace.  splits == POM_GEMM_STREAM_K
@@ -283,8 +284,8 @@ typedef enum { POM_GEMM_K_CONTIG = 0, POM_GEMM_MN_CONTIG = 1 } pom_gemm_layout;
 
 /* The tile and split count pom_gemm uses for this shape and these layouts
  * when asked to choose (a measured table for the baseline configurations'
- * weight gradients, else a cost model); returns POM_ERR_UNSUPPORTED if no
- * tile divides (M, N).  pom_gemm_workspace_size with tile < 0 reports the
+ * weight gradients, else a cost model); returns POM_ERR_UNSUPPORTED if M or
+ * N is not a multiple of 8.  pom_gemm_workspace_size with tile < 0 reports the
  * largest need of the four layouts' plans. */
 int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, int* tile, int* splits);
 size_t pom_gemm_workspace_size(int64_t M, int64_t N, int64_t K, int tile, int splits);

@@ -901,12 +901,13 @@ struct GemmCost {
 // Modelled time of one (tile, splits) choice: whole rounds of 256 workgroups
 // (one per CU) of the per-workgroup time, plus the fixed-order reduction of
 // the fp32 partials when split.  Smaller tiles run the matrix cores less
-// efficiently (more LDS and L2 traffic per flop).
+// efficiently (more LDS and L2 traffic per flop); a partial edge tile costs a
+// whole one.
 double gemm_model_us(int64_t M, int64_t N, int64_t K, int tile, int splits) {
   int bm, bn;
   pom::gemm_tile_dims(tile, &bm, &bn);
   static const double tile_rate[pom::GEMM_TILE_COUNT] = {1.0, 0.97, 0.97, 0.88, 0.88, 0.7};
-  const int64_t units = (M / bm) * (N / bn) * splits;
+  const int64_t units = cdiv(M, bm) * cdiv(N, bn) * splits;
   const int64_t rounds = cdiv(units, 256);
   const double cu_flops = 4.0 * 1024 * 2.1e9 * 0.7 * tile_rate[tile];   // per CU per second
   const double wg_us = 2.0 * bm * bn * ((double)K / splits) / cu_flops * 1e6
@@ -916,7 +917,17 @@ double gemm_model_us(int64_t M, int64_t N, int64_t K, int tile, int splits) {
   return us;
 }
 
+// Every tile takes any M, N that are multiples of 8 (the kernel masks the
+// partial edge tiles); 8-element groups keep the reductions' vector accesses
+// inside a row.  POM_AMD_GEMM_PARTIAL_TILES=0 (read once) admits only tiles
+// that divide M and N.
 bool gemm_tile_fits(int64_t M, int64_t N, int tile) {
+  static const bool partial = [] {
+    const char* e = getenv("POM_AMD_GEMM_PARTIAL_TILES");
+    return !(e && e[0] == '0');
+  }();
+  if (tile < 0 || tile >= pom::GEMM_TILE_COUNT || M % 8 || N % 8) return false;
+  if (partial) return true;
   int bm, bn;
   pom::gemm_tile_dims(tile, &bm, &bn);
   return M % bm == 0 && N % bn == 0;
@@ -935,7 +946,7 @@ size_t gemm_ws_bytes(int64_t M, int64_t N, int tile, int splits) {
 bool gemm_streamk_fits(int64_t M, int64_t N, int64_t K, int tile) {
   int bm, bn;
   pom::gemm_tile_dims(tile, &bm, &bn);
-  return (M / bm) * (N / bn) * (K / 64) >= pom::kStreamKGroups;
+  return cdiv(M, bm) * cdiv(N, bn) * (K / 64) >= pom::kStreamKGroups;
 }
 
 // Measured best (tile, splits) for the weight-gradient products of the baseline configurations
@@ -953,6 +964,7 @@ struct GemmTuned {
 const GemmTuned kGemmTuned[] = {
     {1152, 2304, 16384, 1, 1, 2, 4, -1},  // config 2: dW_ag = g^T sh
     {4608, 1152, 16384, 1, 1, 1, 2, -1},  // config 2: dW_qc = dY^T x
+    {2368, 1152, 16384, 1, 1, 1, 4, -1},  // config 2 with 16 gate heads: dW_qc (10 row tiles, the last partial)
     {1024, 2048, 65536, 1, 1, 0, 8, -1},  // config 3
     {4096, 1024, 65536, 1, 1, 0, 4, -1},
     {1024, 4096, 65536, 1, 1, 0, 4, -1},  // config 4
@@ -1013,7 +1025,7 @@ int pom_gemm_plan(int64_t M, int64_t N, int64_t K, int a_layout, int b_layout, i
   if (M <= 0 || N <= 0 || K <= 0 || K % 64) return fail(POM_ERR_UNSUPPORTED, "gemm: K (%lld) must be a positive multiple of 64", (long long)K);
   const GemmCost c = gemm_choose(M, N, K, a_layout, b_layout);
   if (c.tile < 0)
-    return fail(POM_ERR_UNSUPPORTED, "gemm: no tile divides M=%lld, N=%lld", (long long)M, (long long)N);
+    return fail(POM_ERR_UNSUPPORTED, "gemm: M=%lld and N=%lld must be multiples of 8", (long long)M, (long long)N);
   if (tile) *tile = c.tile;
   if (splits) *splits = c.splits;
   return POM_OK;
@@ -1060,7 +1072,8 @@ int pom_gemm(int a_layout, int b_layout, int64_t M, int64_t N, int64_t K, const 
     if (splits <= 0) splits = c.splits;
   }
   if (tile < 0 || tile >= pom::GEMM_TILE_COUNT || !gemm_tile_fits(M, N, tile))
-    return fail(POM_ERR_UNSUPPORTED, "gemm: tile %d does not divide M=%lld, N=%lld", tile, (long long)M, (long long)N);
+    return fail(POM_ERR_UNSUPPORTED, "gemm: tile %d with M=%lld, N=%lld (tile ids 0-5; M and N multiples of 8)", tile,
+                (long long)M, (long long)N);
   if (splits == pom::GEMM_STREAM_K) {
     if (!gemm_streamk_fits(M, N, K, tile))
       return fail(POM_ERR_UNSUPPORTED, "gemm: stream-K needs tiles x K / 64 >= %d", pom::kStreamKGroups);

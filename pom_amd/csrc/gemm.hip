@@ -21,7 +21,11 @@
 //     has two steps to land; one workgroup barrier per step, which waits
 //     for LDS traffic only (the global loads stay in flight across it);
 //   * operand loads are buffer loads: a wave-uniform descriptor, one 32-bit
-//     offset per thread, the k advance and row steps in the scalar offset;
+//     offset per thread, the k advance and row steps in the scalar offset.
+//     The descriptor's size ends at the operand's last element, so a partial
+//     edge tile (M or N not a multiple of the tile) never reads past it: rows
+//     and columns beyond M / N read zeros or other in-bounds elements, which
+//     only reach outputs the epilogue does not store;
 //   * LDS layout of an operand (R rows x 64 k): four sub-arrays, one per
 //     16-k sub-step, each R rows of 32 bytes plus 32 bytes of padding, rows
 //     and halves permuted within row octets (lds_addr) so that fragment
@@ -344,6 +348,8 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, char* smem, int t, 
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = (LOCAL ? 0 : n0) + wn * WN + 32 * j + 8 * q + 4 * lhalf;
+        // edge tiles: rows past M and columns past N (groups of 4, N a multiple of 8) are not stored
+        if (!LOCAL && (m >= g.M || n >= g.N)) continue;
         if constexpr (OUT_F32) {
           float* c = static_cast<float*>(cout) + m * ldc + n;
           f32x4_t v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
@@ -512,8 +518,8 @@ hipError_t gemm_bf16(const GemmProblem& p, hipStream_t st) {
   g.N = (int)p.N;
   g.nk = (int)(p.K / kBK);
   g.splits = p.splits;
-  g.tiles_m = (int)(p.M / bm);
-  g.tiles_n = (int)(p.N / bn);
+  g.tiles_m = (int)((p.M + bm - 1) / bm);   // the last row / column tile may be partial
+  g.tiles_n = (int)((p.N + bn - 1) / bn);
   const bool sk = p.splits == GEMM_STREAM_K;
   const bool direct = p.splits == 1;
   const bool f32 = p.out_f32 || !direct;

@@ -349,19 +349,24 @@ def test_gemm_plan_and_validation_before_launch(lib):
     import ctypes
     from pom_amd import _lib
     t, sp = ctypes.c_int(-5), ctypes.c_int(-5)
-    # config 2's six projection shapes all have a dividing tile
+    # config 2's six projection shapes all have a plan
     for M, N, K in ((16384, 4608, 1152), (16384, 1152, 2304), (16384, 2304, 1152), (16384, 1152, 4608),
                     (1152, 2304, 16384), (4608, 1152, 16384)):
         assert lib.pom_gemm_plan(M, N, K, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_OK
         assert 0 <= t.value < 6 and (1 <= sp.value <= 8 or sp.value == _lib.GEMM_STREAM_K)
         assert (lib.pom_gemm_workspace_size(M, N, K, -1, 0) > 0) == (sp.value > 1)
-    # no tile divides a 64-multiple like 2368 x 1152 (per-head W at config 2); K must be a multiple of 64
-    assert lib.pom_gemm_plan(2368, 1152, 16384, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_ERR_UNSUPPORTED
+    # a width no tile divides (per-head W = 2368 at config 2) runs with a partial last tile; M and N must be
+    # multiples of 8 and K of 64
+    assert lib.pom_gemm_plan(2368, 1152, 16384, 1, 1, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_OK
+    assert 0 <= t.value < 6
+    assert lib.pom_gemm_plan(2364, 1152, 16384, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_ERR_UNSUPPORTED
+    assert lib.pom_gemm_plan(2368, 1156, 16384, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_ERR_UNSUPPORTED
     assert lib.pom_gemm_plan(1024, 1024, 100, 0, 0, ctypes.byref(t), ctypes.byref(sp)) == _lib.POM_ERR_UNSUPPORTED
     assert lib.pom_gemm_workspace_size(1024, 1024, 4096, 5, 3) == 3 * 1024 * 1024 * 4
     assert lib.pom_gemm_workspace_size(1024, 1024, 4096, 5, 1) == 0
     # stream-K: one fp32 128 x 128 partial per (tile, workgroup) segment, at most 64 tiles + 255
     assert lib.pom_gemm_workspace_size(1024, 1024, 4096, 5, _lib.GEMM_STREAM_K) == (64 + 255) * 128 * 128 * 4
+    assert lib.pom_gemm_workspace_size(1032, 1024, 4096, 5, _lib.GEMM_STREAM_K) == (72 + 255) * 128 * 128 * 4
     fake = 1 << 20   # never dereferenced: every call below fails validation before any launch
     call = lambda al, bl, M, N, K, odt, tile, splits, ws=None, wsb=0, **kw: lib.pom_gemm(
         al, bl, M, N, K, kw.get("A", fake), kw.get("lda", 1024), kw.get("B", fake), kw.get("ldb", 1024), odt,
@@ -372,7 +377,8 @@ def test_gemm_plan_and_validation_before_launch(lib):
     assert call(0, 0, 256, 256, 64, 1, 0, 1, A=0) == _lib.POM_ERR_INVALID     # null operand
     assert call(0, 0, 256, 256, 2048, 1, 0, 1, lda=1000) == _lib.POM_ERR_INVALID    # lda < K
     assert call(0, 0, 256, 256, 64, 1, 0, 1, lda=1028) == _lib.POM_ERR_UNSUPPORTED  # 16-byte rows
-    assert call(0, 0, 192, 256, 64, 1, 0, 1) == _lib.POM_ERR_UNSUPPORTED      # tile 0 does not divide M
+    assert call(0, 0, 196, 256, 64, 1, 0, 1) == _lib.POM_ERR_UNSUPPORTED      # M not a multiple of 8
+    assert call(0, 0, 192, 256, 64, 1, 6, 1) == _lib.POM_ERR_UNSUPPORTED      # tile id
     assert call(0, 0, 256, 256, 640, 1, 0, 9) == _lib.POM_ERR_UNSUPPORTED     # too many splits
     assert call(0, 0, 256, 256, 640, 1, 0, 2) == _lib.POM_ERR_WORKSPACE       # split-K needs workspace
     # stream-K needs at least one 64-step per workgroup: 1 tile x 255 steps is too few, 256 enough

@@ -1,8 +1,8 @@
 """pom_gemm (the matrix-core projection GEMM) against torch's fp32 product of
 the same bf16 operands: every operand layout, tile, split count and output
-dtype, pipeline lengths 1-5 and 16 steps, the stream-K schedule, padded
-leading dimensions, strided views, the C2 weight-gradient shapes at full
-size, and determinism."""
+dtype, pipeline lengths 1-5 and 16 steps, the stream-K schedule, partial
+edge tiles, padded leading dimensions, strided views, the C2 weight-gradient
+shapes at full size, and determinism."""
 import ctypes
 
 import pytest
@@ -160,10 +160,39 @@ def test_gemm_stream_k_deterministic_and_padded(device):
         _check(c1, ref, torch.float32, f"stream-K padded tile {tile}")
 
 
-def test_gemm_plan_chooses_a_dividing_tile(device):
+def test_gemm_plan_is_valid(device):
     lib = _lib.load()
-    for (M, N, K) in ((16384, 4608, 1152), (1152, 2304, 16384), (4608, 1152, 16384), (65536, 1024, 4096)):
+    for (M, N, K) in ((16384, 4608, 1152), (1152, 2304, 16384), (4608, 1152, 16384), (65536, 1024, 4096),
+                      (2368, 1152, 16384)):
         t, s = ctypes.c_int(), ctypes.c_int()
         assert lib.pom_gemm_plan(M, N, K, 0, 0, ctypes.byref(t), ctypes.byref(s)) == 0
-        bm, bn = TILES[t.value]
-        assert M % bm == 0 and N % bn == 0 and (1 <= s.value <= K // 64 or s.value == _lib.GEMM_STREAM_K)
+        assert t.value in TILES and (1 <= s.value <= K // 64 or s.value == _lib.GEMM_STREAM_K)
+
+
+@pytest.mark.parametrize("a_mn,b_mn", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("tile", sorted(TILES))
+def test_gemm_partial_edge_tiles(device, a_mn, b_mn, tile):
+    """M and N that the tile does not divide (the last row and column tiles
+    partial, down to 8 of the tile's rows or columns): every output written
+    once, nothing stored past N in a wider C, for direct, split-K and stream-K
+    runs and both output dtypes."""
+    bm, bn = TILES[tile]
+    lib = _lib.load()
+    for M, N in ((bm + 8, bn + 64), (2 * bm - 56, bn - 8), (8, 16)):
+        for K, splits in ((320, 1), (1024, 3), (64 * 256, _lib.GEMM_STREAM_K)):
+            if splits == _lib.GEMM_STREAM_K and -(-M // bm) * -(-N // bn) * (K // 64) < 256:
+                continue
+            a, b = _operands(M, N, K, a_mn, b_mn, device, seed=M + N + K + tile)
+            ref = _reference(a, a_mn, b, b_mn)
+            for out_dtype in (torch.bfloat16, torch.float32):
+                c = torch.full((M, N + 24), float("nan"), dtype=out_dtype, device=device)
+                c[:, N:] = 7.0
+                wsb = lib.pom_gemm_workspace_size(M, N, K, tile, splits)
+                ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=device)
+                rc = lib.pom_gemm(int(a_mn), int(b_mn), M, N, K, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0),
+                                  _lib.dtype_code(c), c.data_ptr(), c.stride(0), tile, splits, ws.data_ptr(), wsb,
+                                  _lib.stream_handle(device))
+                _lib.check(rc, "pom_gemm")
+                what = f"edge tile {bm}x{bn} M{M} N{N} K{K} s{splits} A{int(a_mn)} B{int(b_mn)} {out_dtype}"
+                _check(c[:, :N], ref, out_dtype, what)
+                assert bool((c[:, N:] == 7.0).all()), what + ": columns past N were written"
