@@ -784,6 +784,16 @@ int pom_gate_heads_fwd(int dtype, int param_dtype, int64_t B, int64_t N, int64_t
     if (int r = set_tview(p.sht, sh_t, dtype, ok ? 8 : 1, B, N, "sh_t")) return r;
   }
   p.sh = sh->data; p.shb = sh->stride_b; p.shn = sh->stride_n;
+  // row walk: the plain gate without the channel-major copy, 8-channel chunks
+  // inside one head and one hagg row per batch row, 16-byte sh rows and hagg;
+  // about heads_rows_target x 4 workgroups of whole 8-row steps
+  if (tune().heads_rows && !sh_t && p.mode == pom::MODE_PLAIN && P % 8 == 0 && p.hd % 8 == 0 && p.G == 1 &&
+      aligned(hagg, 16) && aligned(sh->data, 16) && sh->stride_b % 8 == 0 && sh->stride_n % 8 == 0) {
+    const int64_t cols = cdiv(P / 8, pom::kFwdRowLanes);
+    const int64_t want = cdiv(tune().heads_rows_target * 4, B * cols);
+    p.fwd_rows = cdiv(cdiv(N, want > 0 ? want : 1), 8) * 8;
+    if (cdiv(N, p.fwd_rows) > 65535) p.fwd_rows = cdiv(cdiv(N, 65535), 8) * 8;
+  }
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return hip_status(by_dtype(dtype, [&](auto t) { return pom::heads_fwd_t<decltype(t)>(p, st); }),
                     "pom_gate_heads_fwd launch");

@@ -236,6 +236,60 @@ static __global__ void __launch_bounds__(kThreads) heads_bwd_finalize(const Head
 // formed once per tile; the backward reads dsh once, forming both the
 // per-head dot products (over the tile's channels) and the aggregate-gradient
 // sums (over its tokens) from an LDS copy.
+// Forward row walk (plain gate, no channel-major copy, head_dim % 8 == 0, one
+// hagg row per batch row): 32 lanes x 8 channels of a token row, eight rows
+// per workgroup step.  A lane's 8 channels lie in one head, so its hagg chunk
+// and the head's bias are loaded once; each row then costs one gate load and
+// one 16-byte store, the arithmetic of heads_fwd_tile (bit-identical sh).
+template <typename T>
+__global__ void __launch_bounds__(kThreads) heads_fwd_rows(const HeadsParams p) {
+  constexpr int U = 4;                                   // rows per lane in flight
+  constexpr int kSlots = kThreads / kFwdRowLanes;        // token rows per workgroup step
+  const int tid = threadIdx.x, lc = tid % kFwdRowLanes, slot = tid / kFwdRowLanes;
+  const int64_t b = blockIdx.z;
+  const int64_t c0 = ((int64_t)blockIdx.x * kFwdRowLanes + lc) * 8;
+  if (c0 >= p.P) return;   // no barriers below
+  const int64_t n0 = (int64_t)blockIdx.y * p.fwd_rows;
+  const int64_t n1 = n0 + p.fwd_rows < p.N ? n0 + p.fwd_rows : p.N;
+  const int64_t h = c0 / p.hd;
+  float hv[8];
+  VecIO<T, 8>::load(reinterpret_cast<const T*>(p.hagg) + b * p.P + c0, hv);
+  float bias = 0.0f;
+  if (p.bias.ptr) {
+    float bv[1];
+    param_gather<1>(p.bias, [&](int) { return h; }, bv);
+    bias = bv[0];
+  }
+  const T* yb = reinterpret_cast<const T*>(p.ys) + b * p.ysb + h;
+  T* ob = reinterpret_cast<T*>(p.sh) + b * p.shb + c0;
+  for (int64_t n = n0 + slot; n < n1; n += U * kSlots) {
+    T yv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = n + (int64_t)u * kSlots;
+      yv[u] = yb[(r < n1 ? r : n) * p.ysn];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = n + (int64_t)u * kSlots;
+      if (r >= n1) break;
+      const float g = hsig(to_f32<T>(yv[u]) + bias);
+      float o[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) o[v] = g * hv[v];
+      VecIO<T, 8>::store(ob + r * p.shn, o);
+    }
+  }
+}
+
+template <typename T>
+hipError_t heads_rows_fwd(const HeadsParams& p, hipStream_t st) {
+  const dim3 grid((unsigned)((p.P / 8 + kFwdRowLanes - 1) / kFwdRowLanes), (unsigned)((p.N + p.fwd_rows - 1) / p.fwd_rows),
+                  (unsigned)p.B);
+  hipLaunchKernelGGL((heads_fwd_rows<T>), grid, dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 constexpr int kTT = 64, kCT = 64;
 constexpr int kGM = kCT / 8 + 1;   // heads a kCT-channel tile can touch (head_dim >= 8 on this path)
@@ -739,6 +793,7 @@ hipError_t heads_bwd_v(const HeadsParams& p, hipStream_t st) {
 
 template <typename T>
 hipError_t heads_fwd_t(const HeadsParams& p, hipStream_t st) {
+  if (p.fwd_rows > 0) return heads_rows_fwd<T>(p, st);
   if (p.tile) return heads_tile_fwd<T>(p, st);
   if (p.sht.data) return hipErrorInvalidValue;
   POM_V_SWITCH(T, p.V, heads_fwd_v, p, st)

@@ -211,6 +211,9 @@ template <typename T> hipError_t features_bwd_t(const FeatParams& p, hipStream_t
 
 // Per-head gating (n_sel_heads = H > 1): sh[b,n,c] = rot(hardsigmoid(y_s + bias))[h] * hagg[b, n / L, c],
 // h = c / hd, P = H * hd.
+// lanes per token row of the per-head forward row walk (8 channels each)
+constexpr int kFwdRowLanes = 32;
+
 struct HeadsParams {
   int dtype = DT_BF16;
   int mode = MODE_PLAIN;          // PLAIN / ROPE1D / ROPE2D over the H gate channels
@@ -235,6 +238,7 @@ struct HeadsParams {
   ParamOut dbias;                 // (H,); ptr null: not wanted
 
   TrOut sht;                      // channel-major copy of sh (tile path, 16-bit), or none
+  int64_t fwd_rows = 0;           // > 0: forward row walk (heads_fwd_rows), token rows per workgroup
 
   // general path
   int64_t tok_wgs = 1;            // workgroups of the token-row kernel (= bias partial rows)

@@ -70,10 +70,12 @@ def test_heads_plain(device, B, N, P, H, G, dtype):
     _case(device, B, N, P, H, G, dtype)
 
 
-@pytest.mark.parametrize("N,P,H", [(128, 576, 16), (64, 200, 25), (40, 64, 8)])
+@pytest.mark.parametrize("N,P,H", [(128, 576, 16), (64, 200, 25), (40, 64, 8), (264, 2304, 16)])
 def test_heads_channel_major_copy(device, N, P, H):
     """sh and its channel-major copy (P, B*N) from one launch (bf16); shapes the
-    kernels do not build the copy for fall back to the transpose kernel."""
+    kernels do not build the copy for fall back to the transpose kernel.  Without
+    the copy, head_dim 8 and 144 run the forward row walk, whose sh must equal
+    the tile kernel's."""
     g = torch.Generator().manual_seed(9)
     B = 2
     ys = (torch.randn(B, N, H, generator=g) * 2).to(device, torch.bfloat16)
