@@ -2,7 +2,7 @@
 roofline fractions and a CPU baseline, printed as ONE JSON line.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2|c3|c4|c5|c2h]
-                  [--sub-configs c3,c4,c5] [--no-cpu] [--no-flush] [--graph]
+                  [--sub-configs c3,c4,c5,c2h] [--no-cpu] [--no-flush] [--graph]
 
 A step is one forward + backward of one PoM layer over one batch of synthetic
 input that is resident in HBM before the timed region starts (x, upstream
@@ -21,7 +21,7 @@ copy of their output for the backward GEMMs report those copy bytes
 separately ("copy_bytes", "frac_with_copies").
 
 Besides the headline configuration, the same JSON line carries one object per
-other baseline configuration ("configs": C3-C5 by default) with its fwd and
+other configuration ("configs": C3-C5 and c2h by default) with its fwd and
 fwd+bwd tokens/s, its dominant-kernel roofline, the streaming / GEMM group
 fractions and its own CPU baseline.  "mall_flushed" repeats the headline step
 with 1 GiB written before every step (the Infinity Cache and L2 cold at the
@@ -73,7 +73,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    ap.add_argument("--sub-configs", default="c3,c4,c5",
+    ap.add_argument("--sub-configs", default="c3,c4,c5,c2h",
                     help="comma-separated other configurations measured into the same JSON line ('' for none)")
     ap.add_argument("--sub-cpu-seconds", type=float, default=6.0, help="CPU baseline budget per sub-config")
     ap.add_argument("--no-flush", action="store_true", help="skip the MALL-flushed measurements")
@@ -570,7 +570,7 @@ KERNEL_NAMES = {
     "gate_fwd": ["gate_fwd_kernel"],
     "gate_bwd": ["gate_bwd_kernel", "gate_bwd_finalize"],
     "transpose": ["transpose_blocks", "transpose_elems"],   # x^T, g^T and the weights, per step
-    "gate_heads_fwd": ["heads_fwd_kernel", "heads_fwd_tile"],
+    "gate_heads_fwd": ["heads_fwd_kernel", "heads_fwd_tile", "heads_fwd_rows"],
     "gate_heads_bwd": ["heads_bwd_token_kernel", "heads_bwd_hagg_kernel", "heads_bwd_finalize", "heads_bwd_tile",
                        "heads_bwd_dz", "heads_tile_finalize", "heads_bwd_rows"],
 }
