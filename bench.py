@@ -603,6 +603,22 @@ def _is_gemm(name: str) -> bool:
     return "Cijk" in name or "gemm_bf16_kernel" in name
 
 
+def _label_bwd_gemms(names):
+    """Projection of each of a step's four backward GEMM dispatches (in dispatch
+    order).  With both weight gradients on pom_gemm they are told apart by
+    kernel: the library's products are dsh then dx, pom_gemm's dW_ag then dW_qc,
+    whatever their interleaving (dW_ag may be issued first, on the second
+    stream); otherwise by the one-stream order."""
+    own = [i for i, n in enumerate(names) if "gemm_bf16_kernel" in n]
+    if len(names) == 4 and len(own) == 2:
+        lib = [i for i in range(4) if i not in own]
+        out = [None] * 4
+        out[lib[0]], out[lib[1]] = "gemm_ag_dgrad", "gemm_qc_dgrad"
+        out[own[0]], out[own[1]] = "gemm_ag_wgrad", "gemm_qc_wgrad"
+        return out
+    return ["gemm_ag_dgrad", "gemm_ag_wgrad", "gemm_qc_dgrad", "gemm_qc_wgrad"][:len(names)]
+
+
 def _gemm_dispatches(db: str):
     """Dispatch id and library kernel name of each projection GEMM of the last
     complete fwd+bwd step, from the dispatch order: qc_fwd precedes
@@ -619,8 +635,9 @@ def _gemm_dispatches(db: str):
     af = max(i for i, (_, n) in enumerate(seq[:gb]) if "agg_fwd_chunk" in n)
     pre = [i for i, d in enumerate(seq[:af]) if _is_gemm(d[1])]
     idx = [pre[-1]] + [af + i for i, d in enumerate(seq[af:]) if _is_gemm(d[1])][:5]
+    groups = order[:2] + _label_bwd_gemms([seq[i][1] for i in idx[2:]])
     out = {}
-    for g, i in zip(order, idx):
+    for g, i in zip(groups, idx):
         ds = [seq[i][0]]
         if i + 1 < len(seq) and "gemm_splitk_reduce" in seq[i + 1][1]:
             ds.append(seq[i + 1][0])
@@ -712,7 +729,7 @@ def pmc_table(cfg_name, db, counters):
 def trace_summary(trace_dir):
     """Table of a kernel-trace run: calls, average us, share of GPU time, kernel
     (GEMMs labelled with their projection from the dispatch order of the
-    fwd+bwd steps)."""
+    fwd+bwd steps and, in the backward, their kernel: _label_bwd_gemms)."""
     import csv
     stats = list(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_stats.csv"))))
     trace = sorted(csv.DictReader(open(os.path.join(trace_dir, "run_kernel_trace.csv"))),
@@ -730,7 +747,7 @@ def trace_summary(trace_dir):
             continue   # a forward-only pass
         pre = [i for i in range(af) if _is_gemm(seq[i])]
         idx = [pre[-1]] + [i for i in range(af, end) if _is_gemm(seq[i])][:5]
-        for g, i in zip(order, idx):
+        for g, i in zip(order[:2] + _label_bwd_gemms([seq[j] for j in idx[2:]]), idx):
             red = i + 1 < len(seq) and "gemm_splitk_reduce" in seq[i + 1]
             per[g].append(dur[i] + (dur[i + 1] if red else 0.0))
             label.setdefault(seq[i], set()).add(g)
