@@ -16,9 +16,10 @@ reports the kernel that takes the most time per step, and "kernels" reports
 all of them.
 
 Roofline fractions are in algorithmic units: the bytes (or flops) the
-operation itself needs per launch.  Kernels that also write a channel-major
-copy of their output for the backward GEMMs report those copy bytes
-separately ("copy_bytes", "frac_with_copies").
+operation itself needs per launch.  A kernel that also writes a channel-major
+copy of its output for a backward GEMM on hipBLASLt reports the copy bytes
+separately ("copy_bytes", "frac_with_copies"); with the weight gradients on
+pom_gemm no copy is written and the fields are absent.
 
 Besides the headline configuration, the same JSON line carries one object per
 other configuration ("configs": C3-C5 and c2h by default) with its fwd and
@@ -160,6 +161,22 @@ def forward_fn(cfg, extra_dev):
 # Algorithmic work per kernel launch
 # ---------------------------------------------------------------------------
 
+def copies_written(cfg):
+    """(shᵀ, dYᵀ): whether the layer's bf16 training step writes the channel-major
+    copies.  The gate forward writes shᵀ when dW_ag runs on hipBLASLt; the gate and
+    aggregation backward write dYᵀ when dW_qc does.  A weight gradient on pom_gemm
+    reads the token-major operand in place, and no copy is written."""
+    import torch
+    from pom_amd import ops
+    if not (ops._NT_GEMMS and ops._NT_COPIES == "fused"):
+        return False, False
+    B, N, D, E = cfg["B"], cfg["N"], cfg["D"], cfg["E"]
+    T, P, H = B * N, E * D, cfg.get("heads", 1)
+    W = ops._padded_width(P, H if H > 1 else P)
+    return (not ops.hip_gemm_fits("gemm_ag_wgrad", D, P, T, torch.bfloat16),
+            not ops.hip_gemm_fits("gemm_qc_wgrad", W, D, T, torch.bfloat16))
+
+
 def kernel_work(cfg, extra):
     """name -> (bound, algorithmic bytes or flops per launch, what one unit is)."""
     B, N, D, K, E = cfg["B"], cfg["N"], cfg["D"], cfg["K"], cfg["E"]
@@ -176,9 +193,10 @@ def kernel_work(cfg, extra):
     if cfg["variant"] == "rope2d":
         rope_tab = 0   # tables are (64, P/4) fp32: cache resident, not counted
     mask_b = B * N * 4 if cfg["variant"] == "masked" else 0
-    # channel-major copies written in the same pass (16-bit training path)
-    from pom_amd import ops
-    cm = T * P * e if (ops._NT_GEMMS and ops._NT_COPIES == "fused") else 0
+    # channel-major copies written in the same pass: only for a weight gradient that stays on hipBLASLt
+    sh_copy, dy_copy = copies_written(cfg)
+    cm_sh = T * P * e if sh_copy else 0
+    cm = T * P * e if dy_copy else 0
     # name: (bound, algorithmic bytes or flops per launch, channel-major copy bytes written besides)
     w = {
         "gemm_qc_fwd": ("mfma", 2.0 * T * D * Q, 0),
@@ -192,11 +210,11 @@ def kernel_work(cfg, extra):
         # x read for valid tokens, grad_x written for every token, fp32 upstream grad read
         "agg_bwd": ("hbm", float(read_tok * P * e + T * P * e + B * G * P * 4 + mask_b), cm),
         # y_s read, sh written, aggregate read
-        "gate_fwd": ("hbm", float(2 * T * P * e + B * G * P * e), cm),
+        "gate_fwd": ("hbm", float(2 * T * P * e + B * G * P * e), cm_sh),
         # y_s and dsh read, dy_s written, fp32 dhagg written
         "gate_bwd": ("hbm", float(3 * T * P * e + B * G * P * 4), cm),
         # per-head gate: sh written (y_s and hagg are H / P wide per token / row)
-        "gate_heads_fwd": ("hbm", float(T * P * e + T * H * e + B * G * P * e), cm),
+        "gate_heads_fwd": ("hbm", float(T * P * e + T * H * e + B * G * P * e), cm_sh),
         # dsh read once, y_s read, dy_s written, fp32 dhagg written
         "gate_heads_bwd": ("hbm", float(T * P * e + 2 * T * H * e + B * G * P * 4), 0),
         # operand-layout transposes for the backward GEMMs: read + write once
@@ -411,16 +429,17 @@ def stream_kernels_warm_cold(cfg, reps):
     dh = torch.randn(B, 1, P, generator=g).to(dev)
     dy = torch.empty(T, W, device=dev, dtype=torch.bfloat16)
     dy3 = dy.view(B, N, W)
-    dyt = torch.empty(W, T, device=dev, dtype=torch.bfloat16)
-    sht = torch.empty(P, T, device=dev, dtype=torch.bfloat16)
+    sh_copy, dy_copy = copies_written(cfg)   # the copies the layer's step writes, and only those
+    dyt = torch.empty(W, T, device=dev, dtype=torch.bfloat16) if dy_copy else None
+    sht = torch.empty(P, T, device=dev, dtype=torch.bfloat16) if sh_copy else None
     hagg, _ = ops.agg_forward(h, c, K, N)
     calls = {
         "agg_fwd": lambda: ops.agg_forward(h, c, K, N),
         "gate_fwd": lambda: ops.gate_forward(ys, bias, hagg, out_t=sht),
-        "gate_bwd": lambda: ops.gate_backward(ys, bias, hagg, dsh, dy3[..., P:], grad_ys_t=dyt[P:],
-                                              grad_ys_rows=dy[:, P:]),
-        "agg_bwd": lambda: ops.agg_backward(h, c, K, N, dh, dy3[..., :P], grad_x_t=dyt[:P],
-                                            grad_x_rows=dy[:, :P]),
+        "gate_bwd": lambda: ops.gate_backward(ys, bias, hagg, dsh, dy3[..., P:],
+                                              grad_ys_t=None if dyt is None else dyt[P:], grad_ys_rows=dy[:, P:]),
+        "agg_bwd": lambda: ops.agg_backward(h, c, K, N, dh, dy3[..., :P],
+                                            grad_x_t=None if dyt is None else dyt[:P], grad_x_rows=dy[:, :P]),
     }
     flush = _flusher(dev)
     work = kernel_work(cfg, {})
@@ -442,11 +461,13 @@ def stream_kernels_warm_cold(cfg, reps):
             torch.cuda.synchronize()
             res[mode] = sum(a.elapsed_time(b) for a, b in evs) / reps * 1e-3
         _, amount, copy = work[name]
-        out[name] = {"bytes": amount, "copy_bytes": copy,
+        out[name] = {"bytes": amount,
                      "warm_us": round(res["warm"] * 1e6, 2), "cold_us": round(res["cold"] * 1e6, 2),
                      "warm_frac": round(amount / res["warm"] / HBM_PEAK, 4),
-                     "cold_frac": round(amount / res["cold"] / HBM_PEAK, 4),
-                     "cold_frac_with_copies": round((amount + copy) / res["cold"] / HBM_PEAK, 4)}
+                     "cold_frac": round(amount / res["cold"] / HBM_PEAK, 4)}
+        if copy:
+            out[name]["copy_bytes"] = copy
+            out[name]["cold_frac_with_copies"] = round((amount + copy) / res["cold"] / HBM_PEAK, 4)
     return out
 
 
@@ -805,11 +826,12 @@ def _groups(kernels, work):
     b_hbm = sum(work[n][1] for n in agg)
     c_hbm = sum(work[n][2] for n in agg)
     f_mf = sum(work[n][1] for n in gem)
+    hbm = {"us_per_step": round(t_hbm, 2),
+           "frac_hbm": round(b_hbm / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None}
+    if c_hbm and t_hbm:
+        hbm["frac_hbm_with_copies"] = round((b_hbm + c_hbm) / (t_hbm * 1e-6) / HBM_PEAK, 4)
     return {
-        "hip_streaming_kernels": {"us_per_step": round(t_hbm, 2),
-                                  "frac_hbm": round(b_hbm / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None,
-                                  "frac_hbm_with_copies":
-                                      round((b_hbm + c_hbm) / (t_hbm * 1e-6) / HBM_PEAK, 4) if t_hbm else None},
+        "hip_streaming_kernels": hbm,
         "projection_gemms": {"us_per_step": round(t_mf, 2),
                              "frac_mfma": round(f_mf / (t_mf * 1e-6) / MFMA_BF16_PEAK, 4) if t_mf else None},
         "ideal_step_us": round((b_hbm / HBM_PEAK + f_mf / MFMA_BF16_PEAK) * 1e6, 2),
