@@ -355,9 +355,13 @@ int overlap_mode(hipStream_t st) {
 }
 
 // a second stream (default priority) and two events per device, made once
+// The second stream of a device and its two events, shared by every caller on that device.  A stream wait binds to
+// the event's latest record when the wait is issued, so each record + wait pair runs under `mu`: another thread
+// re-recording the event between the two would otherwise make this caller wait for that thread's stream instead.
 struct Side {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex mu;
 };
 std::mutex g_side_mu;
 Side g_side[kMaxDevices];
@@ -377,8 +381,9 @@ int side_of(Side*& out) {
   return POM_OK;
 }
 
-// `to` waits for everything enqueued on `from` so far
-int wait_for(hipStream_t to, hipStream_t from, hipEvent_t ev) {
+// `to` waits for everything enqueued on `from` so far (ev is one of sd's events)
+int wait_for(Side* sd, hipStream_t to, hipStream_t from, hipEvent_t ev) {
+  std::lock_guard<std::mutex> lock(sd->mu);
   if (hipEventRecord(ev, from) != hipSuccess || hipStreamWaitEvent(to, ev, 0) != hipSuccess)
     return err(POM_ERR_DEVICE, "pom_layer: stream ordering failed");
   return POM_OK;
@@ -535,7 +540,7 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
     hipStream_t st;
     bool armed = false;
     ~Join() {
-      if (armed) (void)wait_for(st, sd->stream, sd->join);
+      if (armed) (void)wait_for(sd, st, sd->stream, sd->join);
     }
   } join{sd, st};
   auto* y = static_cast<__hip_bfloat16*>(a->y);
@@ -543,7 +548,7 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   if (!a->wa_t) return err(POM_ERR_INVALID, "pom_layer_bwd: null wa_t");
   // dW_ag = g^T sh, on the second stream beside the data-gradient chain
   if (side_wa) {
-    if (int r = wait_for(sd->stream, st, sd->fork)) return r;
+    if (int r = wait_for(sd, sd->stream, st, sd->fork)) return r;
     join.armed = true;
     if (int r = pom_gemm(POM_GEMM_MN_CONTIG, POM_GEMM_MN_CONTIG, D, P, T, a->g, D, a->sh, P, a->dwa_dtype, a->dwa, P,
                          -1, 0, wga, wgab, sd->stream))
@@ -620,7 +625,7 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   }
   // dW_qc = dY^T x on the second stream beside dx (both only read dY)
   if (side_wq) {
-    if (int r = wait_for(sd->stream, st, sd->fork)) return r;
+    if (int r = wait_for(sd, sd->stream, st, sd->fork)) return r;
     join.armed = true;
     if (int r = pom_gemm(POM_GEMM_MN_CONTIG, POM_GEMM_MN_CONTIG, W, D, T, a->dy, W, a->x, D, a->dwq_dtype, a->dwq, D,
                          -1, 0, wgq, wgqb, sd->stream))
@@ -645,7 +650,7 @@ int pom_layer_bwd(const pom_layer_args* a, void* stream) {
   }
   if (join.armed) {   // the caller's stream sees the second stream's work done
     join.armed = false;
-    if (int r = wait_for(st, sd->stream, sd->join)) return r;
+    if (int r = wait_for(sd, st, sd->stream, sd->join)) return r;
   }
   return POM_OK;
 }
