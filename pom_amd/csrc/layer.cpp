@@ -371,11 +371,20 @@ int side_of(Side*& out) {
   if (int r = current_device(dev)) return r;
   std::lock_guard<std::mutex> lock(g_side_mu);
   Side& s = g_side[dev];
-  if (!s.stream) {
-    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess)
+  if (!s.stream) {   // published only when the stream and both events exist
+    hipStream_t stream = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&join, hipEventDisableTiming) != hipSuccess) {
+      if (join) (void)hipEventDestroy(join);
+      if (fork) (void)hipEventDestroy(fork);
+      if (stream) (void)hipStreamDestroy(stream);
       return err(POM_ERR_DEVICE, "pom_layer: second stream creation failed");
+    }
+    s.fork = fork;
+    s.join = join;
+    s.stream = stream;
   }
   out = &s;
   return POM_OK;
