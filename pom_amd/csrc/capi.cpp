@@ -966,18 +966,24 @@ bool gemm_streamk_fits(int64_t M, int64_t N, int64_t K, int tile) {
 // together, and the L2 reuse of the lockstep split-K grid is lost.  In the layer that costs more
 // than the idle CUs it fills everywhere but config 4's dW_qc (882-887 us against 908-912); e.g.
 // config 5's dW_qc 677-681 against 609-612, config 2 isolated 236 against 202.
+// dW_ag runs on pom_layer_bwd's second stream beside the data-gradient chain, where fewer splits than the
+// isolated best leave compute units to that chain and write fewer fp32 partials.  Its split counts were chosen
+// inside the layer's backward (same box, three alternating rounds).  Config 2: 2 splits, 0.930-0.932 ms per step
+// against 0.942-0.945 with 4 (0.681-0.683 against 0.707-0.715 with 16 gate heads; 1 split 0.99).  Config 3: 4
+// against 8, 2.331-2.337 against 2.358-2.361.  Config 4: 2 against 4, 4.604-4.615 against 4.649-4.666.  Config
+// 5: 4 against 7 was mixed, so 7 is kept.
 // sk_tile >= 0: stream-K on that tile, unless POM_AMD_GEMM_STREAMK=0 asks for (tile, splits).
 struct GemmTuned {
   int64_t M, N, K;
   int a_layout, b_layout, tile, splits, sk_tile;
 };
 const GemmTuned kGemmTuned[] = {
-    {1152, 2304, 16384, 1, 1, 2, 4, -1},  // config 2: dW_ag = g^T sh
+    {1152, 2304, 16384, 1, 1, 2, 2, -1},  // config 2: dW_ag = g^T sh
     {4608, 1152, 16384, 1, 1, 1, 2, -1},  // config 2: dW_qc = dY^T x
     {2368, 1152, 16384, 1, 1, 1, 4, -1},  // config 2 with 16 gate heads: dW_qc (10 row tiles, the last partial)
-    {1024, 2048, 65536, 1, 1, 0, 8, -1},  // config 3
+    {1024, 2048, 65536, 1, 1, 0, 4, -1},  // config 3
     {4096, 1024, 65536, 1, 1, 0, 4, -1},
-    {1024, 4096, 65536, 1, 1, 0, 4, -1},  // config 4
+    {1024, 4096, 65536, 1, 1, 0, 2, -1},  // config 4
     {8192, 1024, 65536, 1, 1, 0, 4, 0},
     {1536, 3072, 32768, 1, 1, 0, 7, -1},  // config 5
     {6144, 1536, 32768, 1, 1, 0, 3, -1},

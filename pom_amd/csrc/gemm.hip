@@ -373,10 +373,14 @@ template <int BM, int BN, bool A_MN, bool B_MN, bool OUT_F32, bool SK>
 __global__ __launch_bounds__(kThreads, 1) void gemm_bf16_kernel(GemmArgs g) {
   constexpr int STAGE = opnd_bytes<BM>() + opnd_bytes<BN>();
   __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-  // workgroups reach the 8 XCDs round-robin: give each XCD a contiguous run of work
+  // workgroups reach the 8 XCDs round-robin: give each XCD a contiguous run of work.  XCD x receives the
+  // workgroups x, x + 8, ...: total / 8 of them, one more when x < total % 8, mapped to one run of indices.
   const int total = (int)gridDim.x;
   int bid = (int)blockIdx.x;
-  if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  {
+    const int q = total >> 3, r = total & 7, x = bid & 7;
+    bid = x * q + (x < r ? x : r) + (bid >> 3);
+  }
   const int ntile = g.tiles_m * g.tiles_n;
   if constexpr (SK) {
     const int64_t I = (int64_t)ntile * g.nk, G = total;
