@@ -971,7 +971,8 @@ bool gemm_streamk_fits(int64_t M, int64_t N, int64_t K, int tile) {
 // inside the layer's backward (same box, three alternating rounds).  Config 2: 2 splits, 0.930-0.932 ms per step
 // against 0.942-0.945 with 4 (0.681-0.683 against 0.707-0.715 with 16 gate heads; 1 split 0.99).  Config 3: 4
 // against 8, 2.331-2.337 against 2.358-2.361.  Config 4: 2 against 4, 4.604-4.615 against 4.649-4.666.  Config
-// 5: 4 against 7 was mixed, so 7 is kept.
+// 5: 2 against 7, 2.605-2.614 against 2.627-2.636 (4 and 3 were mixed).  Config 2's other shapes measured slower
+// (3 splits, the 256 x 192 tile with 2, the 128 x 128 tile unsplit).
 // sk_tile >= 0: stream-K on that tile, unless POM_AMD_GEMM_STREAMK=0 asks for (tile, splits).
 struct GemmTuned {
   int64_t M, N, K;
@@ -985,7 +986,7 @@ const GemmTuned kGemmTuned[] = {
     {4096, 1024, 65536, 1, 1, 0, 4, -1},
     {1024, 4096, 65536, 1, 1, 0, 2, -1},  // config 4
     {8192, 1024, 65536, 1, 1, 0, 4, 0},
-    {1536, 3072, 32768, 1, 1, 0, 7, -1},  // config 5
+    {1536, 3072, 32768, 1, 1, 0, 2, -1},  // config 5
     {6144, 1536, 32768, 1, 1, 0, 3, -1},
 };
 
